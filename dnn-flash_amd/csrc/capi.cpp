@@ -1,0 +1,481 @@
+// C ABI of the attention forward library (include/onednn_flash_hip.h):
+// argument validation with the reference's error texts, layout resolution,
+// kernel choice, scratch management and the host-buffer convenience entry.
+
+#include "onednn_flash_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "ofh_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int set_error(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+#define OFH_HIP_CHECK(expr)                                                                   \
+    do {                                                                                      \
+        const hipError_t e_ = (expr);                                                         \
+        if (e_ != hipSuccess)                                                                 \
+            return set_error(OFH_ERROR_HIP, std::string(#expr " failed: ") + hipGetErrorString(e_)); \
+    } while (0)
+
+size_t elem_size(int dtype) { return dtype == OFH_DTYPE_F32 ? 4 : 2; }
+
+struct Resolved {
+    int64_t qs[3], ks[3], vs[3], os[3];
+    int algorithm;       // OFH_ALGO_FLASH_MFMA or OFH_ALGO_ROWWISE
+    bool general_mod;    // bias or soft-cap present
+    bool tile_list;      // block-mask tile lists are built
+    int block_n;
+    int num_q_tiles, num_k_tiles;
+};
+
+void contiguous_strides(int64_t out[3], const int64_t in[3], size_t H, size_t T, size_t last) {
+    if (in[0] == 0 && in[1] == 0 && in[2] == 0) {
+        out[2] = (int64_t)last;
+        out[1] = (int64_t)(T * last);
+        out[0] = (int64_t)(H * T * last);
+    } else {
+        out[0] = in[0];
+        out[1] = in[1];
+        out[2] = in[2];
+    }
+}
+
+// All-zero bias strides mean one contiguous [M, N] bias shared by every
+// (batch, head), the shape of the reference's ScoreBiasFn (attention.hpp:31).
+void dense_bias_strides(const ofh_attention_params* p, int64_t out[3]) {
+    if (p->bias_strides[0] == 0 && p->bias_strides[1] == 0 && p->bias_strides[2] == 0) {
+        out[0] = 0;
+        out[1] = 0;
+        out[2] = (int64_t)p->key_tokens;
+    } else {
+        out[0] = p->bias_strides[0];
+        out[1] = p->bias_strides[1];
+        out[2] = p->bias_strides[2];
+    }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Shape and option checks, with the reference's messages where it has one
+// (batched_attention.cpp:15-21, attention.cpp:71-79).
+int validate(const ofh_attention_params* p, bool check_ptrs, const void* q, const void* k,
+             const void* v, const void* out) {
+    if (p == nullptr) return set_error(OFH_ERROR_INVALID_ARGUMENT, "params must be non-null");
+    if (p->struct_size != sizeof(ofh_attention_params))
+        return set_error(OFH_ERROR_INVALID_ARGUMENT,
+                         "ofh_attention_params.struct_size mismatch (call ofh_attention_params_init)");
+    if (check_ptrs && (q == nullptr || k == nullptr || v == nullptr || out == nullptr))
+        return set_error(OFH_ERROR_INVALID_ARGUMENT,
+                         "batched attention input/output pointers must be non-null");
+    if (p->batch == 0 || p->heads == 0 || p->query_tokens == 0 || p->key_tokens == 0 ||
+        p->head_dim == 0 || p->value_dim == 0)
+        return set_error(OFH_ERROR_INVALID_ARGUMENT, "batched attention dimensions must be non-zero");
+    const size_t imax = (size_t)std::numeric_limits<int32_t>::max();
+    if (p->batch > imax || p->heads > imax || p->query_tokens > imax || p->key_tokens > imax ||
+        p->head_dim > imax || p->value_dim > imax || p->batch * p->heads > imax)
+        return set_error(OFH_ERROR_UNSUPPORTED, "attention dimensions exceed the 32-bit index range");
+    if (p->dtype < OFH_DTYPE_F32 || p->dtype > OFH_DTYPE_F16)
+        return set_error(OFH_ERROR_INVALID_ARGUMENT, "unknown dtype");
+    if (p->out_dtype != p->dtype && p->out_dtype != OFH_DTYPE_F32)
+        return set_error(OFH_ERROR_INVALID_ARGUMENT, "out_dtype must equal dtype or be f32");
+    if (!std::isfinite(p->scale))
+        return set_error(OFH_ERROR_INVALID_ARGUMENT, "scale must be finite");
+    if (p->mask_allowed != nullptr) {
+        if (p->mask_query_block_size == 0 || p->mask_key_block_size == 0)
+            return set_error(OFH_ERROR_INVALID_ARGUMENT, "BlockMask block sizes must be non-zero");
+        if (p->mask_query_blocks == 0 || p->mask_key_blocks == 0)
+            return set_error(OFH_ERROR_INVALID_ARGUMENT, "BlockMask dimensions must be non-zero");
+        if (p->mask_query_block_size > imax || p->mask_key_block_size > imax ||
+            p->mask_query_blocks > imax || p->mask_key_blocks > imax)
+            return set_error(OFH_ERROR_UNSUPPORTED, "BlockMask dimensions exceed the 32-bit index range");
+    }
+    if (p->bias_kind < OFH_BIAS_NONE || p->bias_kind > OFH_BIAS_DENSE)
+        return set_error(OFH_ERROR_INVALID_ARGUMENT, "unknown bias kind");
+    if (p->bias_kind == OFH_BIAS_ALIBI && p->alibi_slopes == nullptr)
+        return set_error(OFH_ERROR_INVALID_ARGUMENT, "ALiBi bias needs per-head slopes");
+    if (p->bias_kind == OFH_BIAS_DENSE && p->bias == nullptr)
+        return set_error(OFH_ERROR_INVALID_ARGUMENT, "dense bias needs a bias tensor");
+    if (!(p->softcap >= 0.0f) || !std::isfinite(p->softcap))
+        return set_error(OFH_ERROR_INVALID_ARGUMENT, "softcap must be finite and >= 0");
+    if (p->algorithm < OFH_ALGO_AUTO || p->algorithm > OFH_ALGO_ROWWISE)
+        return set_error(OFH_ERROR_INVALID_ARGUMENT, "unknown algorithm");
+    return OFH_SUCCESS;
+}
+
+int resolve(const ofh_attention_params* p, const void* q, const void* k, const void* v,
+            const void* out, Resolved& r) {
+    contiguous_strides(r.qs, p->q_strides, p->heads, p->query_tokens, p->head_dim);
+    contiguous_strides(r.ks, p->k_strides, p->heads, p->key_tokens, p->head_dim);
+    contiguous_strides(r.vs, p->v_strides, p->heads, p->key_tokens, p->value_dim);
+    contiguous_strides(r.os, p->o_strides, p->heads, p->query_tokens, p->value_dim);
+    r.general_mod = p->bias_kind != OFH_BIAS_NONE || p->softcap > 0.0f;
+
+    // The MFMA kernels read and write 16-byte row chunks.
+    const size_t es = elem_size(p->dtype), oes = elem_size(p->out_dtype);
+    auto strides_ok = [](const int64_t s[3], size_t esz) {
+        for (int i = 0; i < 3; ++i)
+            if (((s[i] * (int64_t)esz) & 15) != 0) return false;
+        return true;
+    };
+    const bool mfma_ok = p->head_dim == p->value_dim &&
+                         (p->head_dim == 64 || p->head_dim == 128) &&
+                         (p->dtype != OFH_DTYPE_F32 || p->out_dtype == OFH_DTYPE_F32) &&
+                         aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) &&
+                         strides_ok(r.qs, es) && strides_ok(r.ks, es) && strides_ok(r.vs, es) &&
+                         strides_ok(r.os, oes);
+    if (p->algorithm == OFH_ALGO_FLASH_MFMA && !mfma_ok)
+        return set_error(OFH_ERROR_UNSUPPORTED,
+                         "flash MFMA kernel needs head_dim == value_dim in {64, 128} and 16-byte "
+                         "aligned rows; use OFH_ALGO_AUTO or OFH_ALGO_ROWWISE");
+    if (p->algorithm == OFH_ALGO_ROWWISE || !mfma_ok) {
+        r.algorithm = OFH_ALGO_ROWWISE;
+        if (p->head_dim > 1024)
+            return set_error(OFH_ERROR_UNSUPPORTED, "rowwise kernel supports head_dim <= 1024");
+        r.tile_list = false;
+        r.block_n = 0;
+        r.num_q_tiles = 0;
+        r.num_k_tiles = 0;
+        return OFH_SUCCESS;
+    }
+    r.algorithm = OFH_ALGO_FLASH_MFMA;
+    r.block_n = ofh::flash_mfma_block_n(p->dtype);
+    r.num_q_tiles = (int)((p->query_tokens + ofh::kBlockM - 1) / ofh::kBlockM);
+    r.num_k_tiles = (int)((p->key_tokens + r.block_n - 1) / r.block_n);
+    r.tile_list = p->mask_allowed != nullptr;
+    const int64_t grid = (int64_t)p->batch * p->heads * r.num_q_tiles;
+    if (grid > std::numeric_limits<int32_t>::max())
+        return set_error(OFH_ERROR_UNSUPPORTED, "grid exceeds 2^31 workgroups");
+    if (r.tile_list && (int64_t)r.num_q_tiles * r.num_k_tiles > (int64_t)1 << 31)
+        return set_error(OFH_ERROR_UNSUPPORTED, "block-mask tile list too large");
+    return OFH_SUCCESS;
+}
+
+size_t workspace_bytes_for(const Resolved& r) {
+    if (!r.tile_list) return 0;
+    const size_t counts = ((size_t)r.num_q_tiles * 4 + 255) & ~size_t(255);
+    return counts + (size_t)r.num_q_tiles * (size_t)r.num_k_tiles * 4;
+}
+
+// Library-owned scratch per device, used when the caller passes no workspace.
+struct DeviceScratch {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_scratch_mu;
+std::map<int, DeviceScratch> g_scratch;
+
+int library_scratch(size_t bytes, void** out) {
+    int dev = 0;
+    OFH_HIP_CHECK(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    DeviceScratch& s = g_scratch[dev];
+    if (s.bytes < bytes) {
+        if (s.ptr != nullptr) {
+            OFH_HIP_CHECK(hipDeviceSynchronize());  // earlier launches may still use it
+            OFH_HIP_CHECK(hipFree(s.ptr));
+            s.ptr = nullptr;
+            s.bytes = 0;
+        }
+        const size_t grown = std::max(bytes, (size_t)1 << 20);
+        OFH_HIP_CHECK(hipMalloc(&s.ptr, grown));
+        s.bytes = grown;
+    }
+    *out = s.ptr;
+    return OFH_SUCCESS;
+}
+
+ofh::FwdArgs make_args(const ofh_attention_params* p, const Resolved& r, const void* q,
+                       const void* k, const void* v, void* out) {
+    ofh::FwdArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.o = out;
+    a.q_sb = r.qs[0]; a.q_sh = r.qs[1]; a.q_sm = r.qs[2];
+    a.k_sb = r.ks[0]; a.k_sh = r.ks[1]; a.k_sn = r.ks[2];
+    a.v_sb = r.vs[0]; a.v_sh = r.vs[1]; a.v_sn = r.vs[2];
+    a.o_sb = r.os[0]; a.o_sh = r.os[1]; a.o_sm = r.os[2];
+    a.B = (int)p->batch;
+    a.H = (int)p->heads;
+    a.M = (int)p->query_tokens;
+    a.N = (int)p->key_tokens;
+    a.D = (int)p->head_dim;
+    a.Dv = (int)p->value_dim;
+    a.scale = p->scale;
+    a.scale_log2 = p->scale * 1.4426950408889634f;
+    a.causal = p->causal ? 1 : 0;
+    a.mask = p->mask_allowed;
+    a.mask_qbs = (int)p->mask_query_block_size;
+    a.mask_kbs = (int)p->mask_key_block_size;
+    a.mask_qb = (int)p->mask_query_blocks;
+    a.mask_kb = (int)p->mask_key_blocks;
+    a.num_q_tiles = r.num_q_tiles;
+    a.num_k_tiles = r.num_k_tiles;
+    a.bias_kind = p->bias_kind;
+    a.alibi = p->alibi_slopes;
+    a.bias = p->bias;
+    int64_t bs[3];
+    dense_bias_strides(p, bs);
+    a.bias_sb = bs[0];
+    a.bias_sh = bs[1];
+    a.bias_sm = bs[2];
+    a.softcap = p->softcap;
+    a.inv_softcap = p->softcap > 0.0f ? 1.0f / p->softcap : 0.0f;
+    a.out_f32 = p->out_dtype == OFH_DTYPE_F32 ? 1 : 0;
+    return a;
+}
+
+int fwd_impl(const ofh_attention_params* p, const void* q, const void* k, const void* v,
+             void* out, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (int rc = validate(p, true, q, k, v, out)) return rc;
+    Resolved r;
+    if (int rc = resolve(p, q, k, v, out, r)) return rc;
+    ofh::FwdArgs a = make_args(p, r, q, k, v, out);
+    if (r.algorithm == OFH_ALGO_ROWWISE) {
+        OFH_HIP_CHECK(ofh::launch_rowwise(a, p->dtype, stream));
+        return OFH_SUCCESS;
+    }
+    if (r.tile_list) {
+        const size_t need = workspace_bytes_for(r);
+        void* ws = workspace;
+        if (ws == nullptr) {
+            if (int rc = library_scratch(need, &ws)) return rc;
+        } else if (workspace_bytes < need) {
+            return set_error(OFH_ERROR_WORKSPACE_TOO_SMALL,
+                             "workspace too small: need " + std::to_string(need) + " bytes");
+        }
+        const size_t counts_bytes = ((size_t)r.num_q_tiles * 4 + 255) & ~size_t(255);
+        ofh::TileListArgs t;
+        t.M = a.M;
+        t.N = a.N;
+        t.block_m = ofh::kBlockM;
+        t.block_n = r.block_n;
+        t.causal = a.causal;
+        t.mask = a.mask;
+        t.mask_qbs = a.mask_qbs;
+        t.mask_kbs = a.mask_kbs;
+        t.mask_qb = a.mask_qb;
+        t.mask_kb = a.mask_kb;
+        t.num_q_tiles = r.num_q_tiles;
+        t.num_k_tiles = r.num_k_tiles;
+        t.counts = static_cast<int*>(ws);
+        t.entries = reinterpret_cast<int*>(static_cast<char*>(ws) + counts_bytes);
+        OFH_HIP_CHECK(ofh::launch_tile_lists(t, stream));
+        a.tile_counts = t.counts;
+        a.tile_entries = t.entries;
+    }
+    OFH_HIP_CHECK(ofh::launch_flash_mfma(a, p->dtype, r.general_mod, stream));
+    return OFH_SUCCESS;
+}
+
+// Per-host-thread device staging for ofh_attention_fwd_host (the counterpart
+// of the reference's thread_local AttentionWorkspace, batched_attention.cpp:37).
+struct HostStaging {
+    int device = -1;
+    void* buf = nullptr;
+    size_t bytes = 0;
+    ~HostStaging() {
+        if (buf != nullptr) (void)hipFree(buf);
+    }
+};
+thread_local HostStaging g_staging;
+
+void f32_to_half_bits(const float* in, uint16_t* out, size_t n, int dtype) {
+    for (size_t i = 0; i < n; ++i) {
+        uint32_t x;
+        std::memcpy(&x, &in[i], 4);
+        if (dtype == OFH_DTYPE_BF16) {
+            if ((x & 0x7fffffffu) > 0x7f800000u) {
+                out[i] = (uint16_t)((x >> 16) | 0x40u);
+            } else {
+                x += 0x7fffu + ((x >> 16) & 1u);
+                out[i] = (uint16_t)(x >> 16);
+            }
+        } else {
+            const _Float16 h = (_Float16)in[i];  // round-to-nearest-even
+            std::memcpy(&out[i], &h, 2);
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+void ofh_attention_params_init(ofh_attention_params* p) {
+    if (p == nullptr) return;
+    std::memset(p, 0, sizeof(*p));
+    p->struct_size = sizeof(ofh_attention_params);
+    p->dtype = OFH_DTYPE_F32;
+    p->out_dtype = OFH_DTYPE_F32;
+    p->scale = 1.0f;
+    p->algorithm = OFH_ALGO_AUTO;
+}
+
+int ofh_attention_workspace_bytes(const ofh_attention_params* p, size_t* bytes) {
+    if (bytes == nullptr) return set_error(OFH_ERROR_INVALID_ARGUMENT, "bytes must be non-null");
+    if (int rc = validate(p, false, nullptr, nullptr, nullptr, nullptr)) return rc;
+    // Alignment is not known here; assume aligned buffers (the larger answer).
+    static const char dummy[16] __attribute__((aligned(16))) = {0};
+    Resolved r;
+    if (int rc = resolve(p, dummy, dummy, dummy, dummy, r)) return rc;
+    *bytes = workspace_bytes_for(r);
+    return OFH_SUCCESS;
+}
+
+int ofh_attention_fwd(const ofh_attention_params* p, const void* q, const void* k, const void* v,
+                      void* out, void* workspace, size_t workspace_bytes, void* stream) {
+    return fwd_impl(p, q, k, v, out, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int ofh_attention_fwd_host(const ofh_attention_params* p, const float* q, const float* k,
+                           const float* v, float* out) {
+    if (int rc = validate(p, true, q, k, v, out)) return rc;
+    for (int i = 0; i < 3; ++i) {
+        if (p->q_strides[i] || p->k_strides[i] || p->v_strides[i] || p->o_strides[i])
+            return set_error(OFH_ERROR_INVALID_ARGUMENT,
+                             "host entry takes the contiguous reference layout (strides must be 0)");
+    }
+    const size_t B = p->batch, H = p->heads, M = p->query_tokens, N = p->key_tokens;
+    const size_t D = p->head_dim, Dv = p->value_dim;
+    const size_t es = elem_size(p->dtype);
+    const size_t nq = B * H * M * D, nk = B * H * N * D, nv = B * H * N * Dv, no = B * H * M * Dv;
+    auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
+    const size_t mask_n = p->mask_allowed ? p->mask_query_blocks * p->mask_key_blocks : 0;
+    size_t bias_n = 0;
+    if (p->bias_kind == OFH_BIAS_DENSE) {
+        // host dense bias: the strides address a host tensor; stage its full extent
+        int64_t s[3];
+        dense_bias_strides(p, s);
+        bias_n = (size_t)((int64_t)(B - 1) * s[0] + (int64_t)(H - 1) * s[1] +
+                          (int64_t)(M - 1) * s[2] + (int64_t)N);
+    }
+    const size_t alibi_n = p->bias_kind == OFH_BIAS_ALIBI ? H : 0;
+    const size_t off_q = 0, off_k = off_q + up(nq * es), off_v = off_k + up(nk * es);
+    const size_t off_o = off_v + up(nv * es), off_m = off_o + up(no * 4);
+    const size_t off_b = off_m + up(mask_n), off_a = off_b + up(bias_n * 4);
+    const size_t total = off_a + up(alibi_n * 4);
+
+    int dev = 0;
+    OFH_HIP_CHECK(hipGetDevice(&dev));
+    HostStaging& st = g_staging;
+    if (st.buf != nullptr && (st.device != dev || st.bytes < total)) {
+        OFH_HIP_CHECK(hipFree(st.buf));
+        st.buf = nullptr;
+        st.bytes = 0;
+    }
+    if (st.buf == nullptr) {
+        OFH_HIP_CHECK(hipMalloc(&st.buf, total));
+        st.bytes = total;
+        st.device = dev;
+    }
+    char* base = static_cast<char*>(st.buf);
+    auto put = [&](size_t off, const float* src, size_t n) -> int {
+        if (p->dtype == OFH_DTYPE_F32) {
+            OFH_HIP_CHECK(hipMemcpy(base + off, src, n * 4, hipMemcpyHostToDevice));
+        } else {
+            std::vector<uint16_t> tmp(n);
+            f32_to_half_bits(src, tmp.data(), n, p->dtype);
+            OFH_HIP_CHECK(hipMemcpy(base + off, tmp.data(), n * 2, hipMemcpyHostToDevice));
+        }
+        return OFH_SUCCESS;
+    };
+    if (int rc = put(off_q, q, nq)) return rc;
+    if (int rc = put(off_k, k, nk)) return rc;
+    if (int rc = put(off_v, v, nv)) return rc;
+    ofh_attention_params dp = *p;
+    dp.out_dtype = OFH_DTYPE_F32;
+    if (mask_n) {
+        OFH_HIP_CHECK(hipMemcpy(base + off_m, p->mask_allowed, mask_n, hipMemcpyHostToDevice));
+        dp.mask_allowed = reinterpret_cast<const uint8_t*>(base + off_m);
+    }
+    if (bias_n) {
+        OFH_HIP_CHECK(hipMemcpy(base + off_b, p->bias, bias_n * 4, hipMemcpyHostToDevice));
+        dp.bias = reinterpret_cast<const float*>(base + off_b);
+    }
+    if (alibi_n) {
+        OFH_HIP_CHECK(hipMemcpy(base + off_a, p->alibi_slopes, alibi_n * 4, hipMemcpyHostToDevice));
+        dp.alibi_slopes = reinterpret_cast<const float*>(base + off_a);
+    }
+    if (int rc = fwd_impl(&dp, base + off_q, base + off_k, base + off_v, base + off_o, nullptr, 0,
+                          nullptr))
+        return rc;
+    OFH_HIP_CHECK(hipMemcpy(out, base + off_o, no * 4, hipMemcpyDeviceToHost));
+    OFH_HIP_CHECK(hipDeviceSynchronize());
+    return OFH_SUCCESS;
+}
+
+int ofh_attention_launch_info(const ofh_attention_params* p, ofh_launch_info* info) {
+    if (info == nullptr) return set_error(OFH_ERROR_INVALID_ARGUMENT, "info must be non-null");
+    if (int rc = validate(p, false, nullptr, nullptr, nullptr, nullptr)) return rc;
+    static const char dummy[16] __attribute__((aligned(16))) = {0};
+    Resolved r;
+    if (int rc = resolve(p, dummy, dummy, dummy, dummy, r)) return rc;
+    std::memset(info, 0, sizeof(*info));
+    info->algorithm = r.algorithm;
+    info->uses_tile_list = r.tile_list ? 1 : 0;
+    const char* name;
+    if (r.algorithm == OFH_ALGO_FLASH_MFMA) {
+        info->block_m = ofh::kBlockM;
+        info->block_n = r.block_n;
+        info->threads = ofh::kThreads;
+        info->workgroups = (int64_t)p->batch * p->heads * r.num_q_tiles;
+        name = ofh::flash_mfma_kernel_name(p->dtype, (int)p->head_dim, r.general_mod);
+    } else {
+        info->block_m = 1;
+        info->block_n = 64;
+        info->threads = 256;
+        info->workgroups = ((int64_t)p->batch * p->heads * p->query_tokens + 3) / 4;
+        name = "rowwise_fwd_kernel";
+    }
+    std::strncpy(info->kernel_name, name, sizeof(info->kernel_name) - 1);
+    return OFH_SUCCESS;
+}
+
+int ofh_attention_useful_flops(const ofh_attention_params* p, double* flops) {
+    if (flops == nullptr) return set_error(OFH_ERROR_INVALID_ARGUMENT, "flops must be non-null");
+    if (int rc = validate(p, false, nullptr, nullptr, nullptr, nullptr)) return rc;
+    const size_t M = p->query_tokens, N = p->key_tokens;
+    double pairs = 0.0;
+    for (size_t i = 0; i < M; ++i) {
+        const size_t kmax = p->causal ? std::min(N, i + 1) : N;  // keys [0, kmax) pass causal
+        if (p->mask_allowed == nullptr) {
+            pairs += (double)kmax;
+            continue;
+        }
+        const size_t qb = i / p->mask_query_block_size;
+        if (qb >= p->mask_query_blocks) continue;
+        const uint8_t* row = p->mask_allowed + qb * p->mask_key_blocks;
+        for (size_t kb = 0; kb < p->mask_key_blocks; ++kb) {
+            if (!row[kb]) continue;
+            const size_t ks = kb * p->mask_key_block_size;
+            const size_t ke = std::min(kmax, ks + p->mask_key_block_size);
+            if (ke > ks) pairs += (double)(ke - ks);
+        }
+    }
+    *flops = 2.0 * (double)(p->head_dim + p->value_dim) * pairs * (double)p->batch * (double)p->heads;
+    return OFH_SUCCESS;
+}
+
+const char* ofh_last_error(void) { return g_last_error.c_str(); }
+
+int ofh_abi_version(void) { return OFH_ABI_VERSION; }
+
+}  // extern "C"

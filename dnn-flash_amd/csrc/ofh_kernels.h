@@ -1,0 +1,72 @@
+// Kernel-side argument block and launcher entry points shared by the HIP
+// translation units of the library. Internal header: not installed.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ofh {
+
+enum DType : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
+enum Bias : int { BIAS_NONE = 0, BIAS_ALIBI = 1, BIAS_DENSE = 2 };
+
+// Tile shape of the MFMA flash kernels: 4 wavefronts, each owning 32 query
+// rows (one 32-wide MFMA column block), K/V streamed in tiles of 64 keys.
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kQueriesPerWave = 32;
+constexpr int kBlockM = kWaves * kQueriesPerWave;  // 128
+constexpr int kBlockN = 64;
+
+// Everything a forward kernel needs, passed by value. Pointers are device
+// pointers; strides are in elements; the last axis of every tensor is
+// contiguous.
+struct FwdArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    int64_t q_sb, q_sh, q_sm;
+    int64_t k_sb, k_sh, k_sn;
+    int64_t v_sb, v_sh, v_sn;
+    int64_t o_sb, o_sh, o_sm;
+    int B, H, M, N, D, Dv;
+    float scale;       // score scale
+    float scale_log2;  // scale * log2(e)
+    int causal;
+    // block mask
+    const uint8_t* mask;
+    int mask_qbs, mask_kbs, mask_qb, mask_kb;
+    // per-query-tile lists of key tiles (block mask only)
+    const int* tile_counts;   // [num_q_tiles]
+    const int* tile_entries;  // [num_q_tiles, num_k_tiles], entry = kt*2 + partial
+    int num_q_tiles, num_k_tiles;
+    // score_mod
+    int bias_kind;
+    const float* alibi;  // [H]
+    const float* bias;
+    int64_t bias_sb, bias_sh, bias_sm;
+    float softcap;      // 0: off
+    float inv_softcap;
+    int out_f32;        // 1: O is fp32, else O has the input dtype
+};
+
+struct TileListArgs {
+    int M, N, block_m, block_n, causal;
+    const uint8_t* mask;
+    int mask_qbs, mask_kbs, mask_qb, mask_kb;
+    int num_q_tiles, num_k_tiles;
+    int* counts;
+    int* entries;
+};
+
+// Launchers; each returns the hipError_t of the launch.
+hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipStream_t s);
+hipError_t launch_rowwise(const FwdArgs& a, int dtype, hipStream_t s);
+hipError_t launch_tile_lists(const TileListArgs& a, hipStream_t s);
+
+const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod);
+// Keys per K/V tile of the MFMA kernel for a dtype (64 for bf16/fp16, 32 for fp32).
+int flash_mfma_block_n(int dtype);
+
+}  // namespace ofh

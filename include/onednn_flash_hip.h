@@ -1,0 +1,163 @@
+/*
+ * onednn_flash_hip.h - C ABI of the MI355X (gfx950) attention forward library.
+ *
+ * Plain C: POD parameters, device pointers and sizes, an int status code, and
+ * a thread-local error string. No C++ exceptions cross this boundary and no
+ * HIP or framework types appear in the signatures (the stream is passed as
+ * void*, a hipStream_t or NULL for the default stream).
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   ofh_attention_fwd            flash_attention_batched_qk_pv_tile
+ *                                (include/onednn_flash/batched_attention.hpp:26-31,
+ *                                 src/onednn_flash/batched_attention.cpp:9-49) and,
+ *                                per head, flash_attention_qk_pv_tile_ws
+ *                                (src/onednn_flash/attention.cpp:486-695)
+ *   ofh_attention_fwd_host       the same entry on host fp32 buffers, as the
+ *                                TensorFlow CPU op calls it
+ *                                (tensorflow_ops/onednn_flash_attention_op.cc:125-134)
+ *   ofh_attention_workspace_bytes
+ *                                AttentionWorkspace::resize
+ *                                (src/onednn_flash/attention_workspace.cpp:5-20)
+ *   OFH_ALGO_ROWWISE             standard_attention
+ *                                (src/onednn_flash/attention.cpp:88-137)
+ *   ofh_last_error               the what() text of the exceptions the reference
+ *                                throws (std::invalid_argument / std::runtime_error)
+ */
+#ifndef ONEDNN_FLASH_HIP_H
+#define ONEDNN_FLASH_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OFH_ABI_VERSION 1
+
+/* Status codes. INVALID_ARGUMENT corresponds to the reference's
+ * std::invalid_argument, the others to std::runtime_error. */
+typedef enum ofh_status {
+    OFH_SUCCESS = 0,
+    OFH_ERROR_INVALID_ARGUMENT = 1,
+    OFH_ERROR_UNSUPPORTED = 2,
+    OFH_ERROR_HIP = 3,
+    OFH_ERROR_WORKSPACE_TOO_SMALL = 4
+} ofh_status;
+
+/* Element type of Q, K, V and O in device memory. */
+typedef enum ofh_dtype {
+    OFH_DTYPE_F32 = 0,
+    OFH_DTYPE_BF16 = 1,
+    OFH_DTYPE_F16 = 2
+} ofh_dtype;
+
+/* Additive score bias, applied after the scale (attention.cpp:106-107, 619). */
+typedef enum ofh_bias_kind {
+    OFH_BIAS_NONE = 0,
+    OFH_BIAS_ALIBI = 1, /* alibi_slopes[h] * (key_index - query_index) */
+    OFH_BIAS_DENSE = 2  /* bias[b*sb + h*sh + q*sq + k], fp32 */
+} ofh_bias_kind;
+
+/* Which kernel family runs. AUTO picks the MFMA flash kernel when the shape
+ * is supported (D == Dv in {64, 128}, 16-byte aligned rows) and the rowwise
+ * kernel otherwise. ROWWISE is the exact two-pass softmax of
+ * standard_attention, run on the GPU one query row per wavefront. */
+typedef enum ofh_algorithm {
+    OFH_ALGO_AUTO = 0,
+    OFH_ALGO_FLASH_MFMA = 1,
+    OFH_ALGO_ROWWISE = 2
+} ofh_algorithm;
+
+typedef struct ofh_attention_params {
+    uint32_t struct_size; /* sizeof(ofh_attention_params), set by ofh_attention_params_init */
+
+    /* BatchedAttentionShape (batched_attention.hpp:9-16). */
+    size_t batch, heads, query_tokens, key_tokens, head_dim, value_dim;
+
+    int32_t dtype;      /* ofh_dtype of q, k, v */
+    int32_t out_dtype;  /* ofh_dtype of out: the input dtype or OFH_DTYPE_F32 */
+
+    /* Element strides for the batch, head and token axes; the last axis is
+     * contiguous. All zero means the reference layout: contiguous
+     * Q[B,H,M,D], K[B,H,N,D], V[B,H,N,Dv], O[B,H,M,Dv] (batched_attention.hpp:18-22). */
+    int64_t q_strides[3], k_strides[3], v_strides[3], o_strides[3];
+
+    float scale; /* AttentionOptions::scale (attention.hpp:40); default 1.0 */
+    int32_t causal; /* top-left aligned: key > query is masked (attention.cpp:54-57) */
+
+    /* BlockMask (attention.hpp:20-29): device pointer to a row-major
+     * [mask_query_blocks, mask_key_blocks] uint8 bitmap, non-zero = allowed.
+     * NULL means no block mask. Blocks out of range are disallowed. */
+    const uint8_t* mask_allowed;
+    size_t mask_query_block_size, mask_key_block_size, mask_query_blocks, mask_key_blocks;
+
+    /* score_mod, fused into the score tile before exponentiation. Order:
+     * s*scale + bias, then softcap*tanh(./softcap) when softcap > 0. Masked
+     * scores get neither. */
+    int32_t bias_kind;           /* ofh_bias_kind */
+    const float* alibi_slopes;   /* device [heads] */
+    const float* bias;           /* device fp32, see bias_strides */
+    int64_t bias_strides[3];     /* batch, head, query-row strides (elements); key stride 1.
+                                    All zero: one contiguous [M, N] bias for every head. */
+    float softcap;               /* <= 0: disabled */
+
+    int32_t algorithm;           /* ofh_algorithm */
+} ofh_attention_params;
+
+/* Fills defaults: struct_size, dtype f32, out_dtype f32, scale 1.0, everything
+ * else zero (no mask, no bias, AUTO). */
+void ofh_attention_params_init(ofh_attention_params* p);
+
+/* Bytes of device scratch the forward call needs for these parameters (the
+ * per-query-tile list of allowed key tiles when a block mask is given; 0
+ * otherwise). */
+int ofh_attention_workspace_bytes(const ofh_attention_params* p, size_t* bytes);
+
+/* Attention forward on device buffers, ordered on `stream` (asynchronous).
+ * workspace may be NULL: the library then uses a per-device buffer it owns,
+ * grown on demand (one hipMalloc the first time a larger size is needed).
+ * Fully-masked query rows are written as zeros, as standard_attention leaves
+ * them (attention.cpp:111-113). */
+int ofh_attention_fwd(const ofh_attention_params* p, const void* q, const void* k,
+                      const void* v, void* out, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+/* The same computation on host fp32 buffers (contiguous reference layout):
+ * copies in, runs on the current device, copies out, synchronises. The dtype
+ * field selects the precision the GPU computes in (inputs are rounded to it
+ * with round-to-nearest-even); out is always fp32. The mask and the ALiBi
+ * slopes / dense bias are host pointers here. Device staging buffers are kept
+ * per host thread and reused (no allocation after the first call of a size). */
+int ofh_attention_fwd_host(const ofh_attention_params* p, const float* q, const float* k,
+                           const float* v, float* out);
+
+/* Describes the launch that ofh_attention_fwd would make. */
+typedef struct ofh_launch_info {
+    int32_t algorithm;        /* OFH_ALGO_FLASH_MFMA or OFH_ALGO_ROWWISE */
+    int32_t block_m;          /* queries per workgroup */
+    int32_t block_n;          /* keys per K/V tile */
+    int32_t threads;          /* threads per workgroup */
+    int64_t workgroups;       /* grid size of the attention kernel */
+    int32_t uses_tile_list;   /* 1 when a block-mask tile list is built first */
+    char kernel_name[96];
+} ofh_launch_info;
+
+int ofh_attention_launch_info(const ofh_attention_params* p, ofh_launch_info* info);
+
+/* Useful FLOPs of the call: 4*D*(unmasked (query,key) pairs)*B*H for D == Dv
+ * (2*(D+Dv)*pairs*B*H in general), counted exactly on the host from the mask.
+ * The mask pointer must be a host pointer here. */
+int ofh_attention_useful_flops(const ofh_attention_params* p, double* flops);
+
+/* Thread-local text of the last error on this thread ("" if none). */
+const char* ofh_last_error(void);
+
+/* OFH_ABI_VERSION the library was built with. */
+int ofh_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ONEDNN_FLASH_HIP_H */
