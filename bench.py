@@ -1,0 +1,213 @@
+#!/usr/bin/env python3
+"""Attention forward benchmark on one MI355X.
+
+A step is one attention forward call (the HIP kernels behind the C ABI) over
+one batch of synthetic device-resident inputs. Default workload: bf16 causal
+attention, B=4 H=32 N=4096 D=128 (the headline configuration). Prints ONE JSON
+line with the useful-FLOP throughput, the roofline figures of the attention
+kernel (per-launch durations measured with HIP events on the launch stream)
+and a CPU baseline: the reference's own CPU flash path (compiled from its
+sources into oracle/_ref) on a bounded sample of the same workload, run on the
+host cores (the oracle's restatement when oracle/_ref is absent).
+
+    python bench.py [--steps K] [--warmup W] [--workload c3] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(ROOT / "dnn-flash_amd" / "python"))
+
+METRIC = "attention fwd TFLOP/s (useful FLOPs) + % bf16 MFMA peak, 1×MI355X"
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c3")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cpu count)")
+    ap.add_argument("--cpu-heads", type=int, default=0, help="heads in the CPU sample; 0: two per thread")
+    return ap.parse_args()
+
+
+def device_inputs(w, torch):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1234)
+    dt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[w.dtype]
+    shape = (w.batch, w.heads, w.tokens, w.head_dim)
+    q, k, v = (torch.randn(shape, device="cuda", generator=g, dtype=torch.float32).mul_(w.std).to(dt)
+               for _ in range(3))
+    out = torch.empty(shape, device="cuda", dtype=dt)
+    return q, k, v, out
+
+
+def traffic_from_profiles(w):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE),
+    scaled by the copy-kernel calibration; stored under profiles/ as JSON."""
+    p = ROOT / "profiles" / f"traffic_{w.name}.json"
+    if not p.exists():
+        return None
+    try:
+        return float(json.loads(p.read_text())["hbm_bytes_per_launch"])
+    except (ValueError, KeyError):
+        return None
+
+
+def cpu_baseline(w, threads: int, nheads: int):
+    import numpy as np
+
+    from oracle import oracle as O
+
+    if nheads <= 0:
+        nheads = 2 * threads
+    nheads = max(1, min(nheads, w.batch * w.heads))
+    # the sampled heads' inputs: same distribution, rounded to the device dtype
+    shape = (1, nheads, w.tokens, w.head_dim)
+    q, k, v = (O.round_to(O.normal(s, shape, std=w.std, threads=threads), w.dtype)[1] for s in (11, 12, 13))
+    prob = O.Problem(1, nheads, w.tokens, w.tokens, w.head_dim, w.head_dim, scale=w.scale,
+                     causal=w.causal, mask=w.mask(), mask_query_block_size=64,
+                     mask_key_block_size=64,
+                     alibi_slopes=w.alibi_slopes()[:nheads] if w.alibi else None,
+                     softcap=w.softcap)
+    heads = np.arange(nheads)
+    q_bs, k_bs = (32, 64) if w.tokens > 64 else (64, 64)  # python/onednn_flash_tf/ops.py:29-31
+    kind = "reference" if O.ref_available() and w.softcap == 0.0 else "port"
+    t0 = time.perf_counter()
+    if kind == "reference":
+        O.ref_flash_heads(q, k, v, prob, heads, q_bs, k_bs, threads=threads)
+    else:
+        O.flash_heads(q, k, v, prob, heads, q_bs, k_bs, threads=threads)
+    dt = time.perf_counter() - t0
+    flops = 4.0 * w.head_dim * w.useful_pairs_per_head() * nheads
+    note = "" if kind == "reference" else " (oracle restatement: the reference has no soft-cap)" if w.softcap else ""
+    return {
+        "value": flops / dt / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": kind,
+        "sample": (f"{nheads} of {w.batch * w.heads} heads of {w.name}, fp32 on {w.dtype}-rounded "
+                   f"inputs, tiles {q_bs}x{k_bs}, {nheads} heads on {threads} threads, {dt:.2f} s wall{note}"),
+    }
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU: the attention kernel shards by heads "
+                                   "with no communication (see DESIGN.md); --gpus must be 1"}))
+        return 2
+
+    import torch
+
+    import onednn_flash_configs as C
+    import onednn_flash_hip as F
+
+    w = C.get(args.workload)
+    torch.cuda.init()
+    q, k, v, out = device_inputs(w, torch)
+    kw = {}
+    mask_t = slopes_t = None
+    m = w.mask()
+    if m is not None:
+        mask_t = torch.from_numpy(m).cuda()
+        kw.update(mask_allowed=mask_t.data_ptr(), mask_query_block_size=64, mask_key_block_size=64,
+                  mask_query_blocks=m.shape[0], mask_key_blocks=m.shape[1])
+    if w.alibi:
+        slopes_t = torch.from_numpy(w.alibi_slopes()).cuda()
+        kw.update(bias_kind=F.BIAS_ALIBI, alibi_slopes=slopes_t.data_ptr())
+    code = {"f32": F.DTYPE_F32, "bf16": F.DTYPE_BF16, "f16": F.DTYPE_F16}[w.dtype]
+    p = F.make_params(w.batch, w.heads, w.tokens, w.tokens, w.head_dim, dtype=code, scale=w.scale,
+                      causal=w.causal, softcap=w.softcap, **kw)
+    info = F.launch_info(p)
+    ws_bytes = F.workspace_bytes(p)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+    lib = F.lib()
+    pp = ctypes.byref(p)
+    qa, ka, va, oa, wsa = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), ws.data_ptr()
+    sh = stream.cuda_stream
+
+    def step():
+        rc = lib.ofh_attention_fwd(pp, qa, ka, va, oa, wsa if ws_bytes else None, ws_bytes, sh)
+        if rc:
+            raise F.OfhError(rc, lib.ofh_last_error().decode())
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # timed region: K steps, an event before every launch and after the last one
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        events[i].record(stream)
+        step()
+    events[-1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_launch = [events[i].elapsed_time(events[i + 1]) for i in range(args.steps)]
+    ms = events[0].elapsed_time(events[-1]) / args.steps
+    avg_launch_ms = sum(per_launch) / len(per_launch)
+
+    flops = w.useful_flops()
+    value = flops / (ms * 1e-3) / 1e12
+    achieved = flops / (avg_launch_ms * 1e-3) / 1e12
+    peak = C.PEAK_TFLOPS[w.dtype]
+    rec = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": w.dtype,
+        "data": f"synthetic iid N(0,{w.std:g}) inputs generated on the device",
+        "config": {
+            "workload": w.name,
+            "batch": w.batch, "heads": w.heads, "tokens": w.tokens, "head_dim": w.head_dim,
+            "causal": w.causal,
+            "block_mask": "64x64 causal window 16 blocks + 4 sinks" if w.block_sparse else None,
+            "score_mod": ("scale+alibi+softcap" if w.alibi and w.softcap else "scale"),
+            "kernel": info.kernel_name.decode(),
+            "useful_gflop": round(flops / 1e9, 3),
+        },
+        "pct_bf16_peak": round(100.0 * value / C.PEAK_TFLOPS["bf16"], 2),
+        "wall_s_timed": round(wall, 4),
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 3),
+            "peak": peak,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / peak, 4),
+            "traffic": traffic_from_profiles(w),
+            "algorithmic_bytes": w.algorithmic_bytes(),
+            "avg_launch_ms": round(avg_launch_ms, 5),
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        rec["cpu_baseline"] = cpu_baseline(w, threads, args.cpu_heads)
+    print(json.dumps(rec))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

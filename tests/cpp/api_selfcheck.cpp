@@ -1,0 +1,153 @@
+// Self-check of the C++ API (include/onednn_flash/*.hpp) on the GPU, the
+// counterpart of the reference's benchmarks/bench_attention.cpp:33-160: every
+// attention entry point against standard_attention on M=N=128, D=64, causal,
+// scale 1/8, inputs sin(0.013 i + {0.1, 1.3, 2.7}) * 0.25, max-abs <= 1e-5.
+// Also exercises the batched and raw-pointer entries, BlockMask, ScoreBiasFn,
+// per-head ALiBi, the tile-GEMM seam and the error contract. Exit code 0 = pass.
+
+#include <cmath>
+#include <cstdio>
+#include <stdexcept>
+#include <vector>
+
+#include "onednn_flash/attention.hpp"
+#include "onednn_flash/backend.hpp"
+#include "onednn_flash/batched_attention.hpp"
+
+namespace of = onednn_flash;
+
+static std::vector<float> sin_values(std::size_t n, float offset) {
+    std::vector<float> v(n);
+    for (std::size_t i = 0; i < n; ++i) v[i] = std::sin(static_cast<float>(i) * 0.013f + offset) * 0.25f;
+    return v;
+}
+
+static int failures = 0;
+static void expect(bool ok, const char* what, double value) {
+    std::printf("%-48s %s (%.3g)\n", what, ok ? "ok" : "FAIL", value);
+    if (!ok) ++failures;
+}
+
+template <typename E, typename Fn>
+static void expect_throw(Fn&& fn, const char* what) {
+    bool thrown = false;
+    try {
+        fn();
+    } catch (const E&) {
+        thrown = true;
+    } catch (...) {
+    }
+    expect(thrown, what, thrown ? 1.0 : 0.0);
+}
+
+int main() {
+    const of::AttentionShape shape{128, 128, 64, 64};
+    const auto q = sin_values(shape.query_tokens * shape.head_dim, 0.1f);
+    const auto k = sin_values(shape.key_tokens * shape.head_dim, 1.3f);
+    const auto v = sin_values(shape.key_tokens * shape.value_dim, 2.7f);
+    const of::AttentionOptions options{1.0f / std::sqrt(static_cast<float>(shape.head_dim)), true, 32};
+
+    const auto standard = of::standard_attention(q, k, v, shape, options);
+    auto tile_opts = options;
+    tile_opts.query_block_size = 16;
+    expect(of::max_abs_diff(standard, of::flash_attention_tiled(q, k, v, shape, options)) <= 1e-5f,
+           "flash_attention_tiled vs standard", of::max_abs_diff(standard, of::flash_attention_tiled(q, k, v, shape, options)));
+    const double d_q = of::max_abs_diff(standard, of::flash_attention_q_tile(q, k, v, shape, tile_opts));
+    expect(d_q <= 1e-5, "flash_attention_q_tile vs standard", d_q);
+    const double d_qkpv = of::max_abs_diff(standard, of::flash_attention_qk_pv_tile(q, k, v, shape, tile_opts));
+    expect(d_qkpv <= 1e-5, "flash_attention_qk_pv_tile vs standard", d_qkpv);
+    const double d_run = of::max_abs_diff(standard, of::run_attention(of::AttentionBackendKind::FlashMfmaHip, q, k, v, shape, options));
+    expect(d_run <= 1e-5, "run_attention(FlashMfmaHip) vs standard", d_run);
+
+    std::vector<float> out_ws(shape.query_tokens * shape.value_dim, -1.0f);
+    of::AttentionWorkspace ws;
+    of::flash_attention_qk_pv_tile_ws(q.data(), k.data(), v.data(), out_ws.data(), shape, tile_opts, ws);
+    void* const first_buffer = ws.device_buffer;
+    of::flash_attention_qk_pv_tile_ws(q.data(), k.data(), v.data(), out_ws.data(), shape, tile_opts, ws);
+    expect(ws.device_buffer == first_buffer, "workspace reused without reallocation", 0.0);
+    expect(of::max_abs_diff(standard, out_ws) <= 1e-5f, "flash_attention_qk_pv_tile_ws vs standard",
+           of::max_abs_diff(standard, out_ws));
+
+    // batched: two heads with different data == two single-head calls
+    const of::BatchedAttentionShape bshape{1, 2, 128, 128, 64, 64};
+    std::vector<float> bq(q), bk(k), bv(v);
+    const auto q2 = sin_values(q.size(), 0.5f), k2 = sin_values(k.size(), 0.9f), v2 = sin_values(v.size(), 1.7f);
+    bq.insert(bq.end(), q2.begin(), q2.end());
+    bk.insert(bk.end(), k2.begin(), k2.end());
+    bv.insert(bv.end(), v2.begin(), v2.end());
+    std::vector<float> bout(2 * 128 * 64);
+    of::flash_attention_batched_qk_pv_tile(bq.data(), bk.data(), bv.data(), bout.data(), bshape, options);
+    const auto second = of::standard_attention(q2, k2, v2, shape, options);
+    const std::vector<float> h0(bout.begin(), bout.begin() + 128 * 64), h1(bout.begin() + 128 * 64, bout.end());
+    expect(of::max_abs_diff(h0, standard) <= 1e-5f && of::max_abs_diff(h1, second) <= 1e-5f,
+           "batched entry vs per-head standard", std::max(of::max_abs_diff(h0, standard), of::max_abs_diff(h1, second)));
+
+    // BlockMask + ScoreBiasFn (ALiBi through the callback) vs per-head ALiBi slopes
+    of::BlockMask bm;
+    bm.query_block_size = 32;
+    bm.key_block_size = 32;
+    bm.query_blocks = 4;
+    bm.key_blocks = 4;
+    bm.allowed = {1, 0, 0, 0, 1, 1, 0, 0, 0, 1, 1, 0, 1, 0, 1, 1};
+    auto mopts = options;
+    mopts.block_mask = &bm;
+    mopts.score_bias = [](std::size_t qi, std::size_t kj) {
+        return 0.25f * static_cast<float>(static_cast<long>(kj) - static_cast<long>(qi));
+    };
+    const auto std_mask = of::standard_attention(q, k, v, shape, mopts);
+    const auto fl_mask = of::flash_attention_tiled(q, k, v, shape, mopts);
+    expect(of::max_abs_diff(std_mask, fl_mask) <= 1e-5f, "block mask + score_bias: flash vs standard",
+           of::max_abs_diff(std_mask, fl_mask));
+    auto aopts = options;
+    aopts.block_mask = &bm;
+    aopts.alibi_slopes = {0.25f};
+    const auto fl_alibi = of::flash_attention_tiled(q, k, v, shape, aopts);
+    expect(of::max_abs_diff(std_mask, fl_alibi) <= 1e-5f, "alibi_slopes == ALiBi ScoreBiasFn",
+           of::max_abs_diff(std_mask, fl_alibi));
+    expect(bm.allows(40, 10) && !bm.allows(10, 40) && !bm.allows(500, 0), "BlockMask::allows", 0.0);
+
+    // tile-GEMM seam: C = A x B and the strided K^T view
+    const of::MatmulShape ms{5, 7, 3};
+    std::vector<float> a(15), b(21);
+    for (int i = 0; i < 15; ++i) a[i] = 0.5f * i - 3.0f;
+    for (int i = 0; i < 21; ++i) b[i] = 0.25f * i - 2.0f;
+    const auto c = of::matmul_tile(of::TileKernelKind::HipMfma, a, b, ms);
+    double gemm_err = 0.0;
+    for (int i = 0; i < 5; ++i)
+        for (int j = 0; j < 7; ++j) {
+            double s = 0.0;
+            for (int kk = 0; kk < 3; ++kk) s += a[i * 3 + kk] * b[kk * 7 + j];
+            gemm_err = std::max(gemm_err, std::fabs(s - c[i * 7 + j]));
+        }
+    expect(gemm_err <= 1e-5, "matmul_tile", gemm_err);
+    std::vector<float> kt(7 * 3);  // K[7,3] row-major, read as B = K^T [3,7]
+    for (int j = 0; j < 7; ++j)
+        for (int kk = 0; kk < 3; ++kk) kt[j * 3 + kk] = b[kk * 7 + j];
+    std::vector<float> cs(35, 0.0f);
+    of::matmul_tile_strided_inplace(of::TileKernelKind::Reference, a.data(), kt.data(), cs.data(),
+                                    of::StridedMatmulShape{5, 7, 3, 3, 1, 1, 3, 7, 1});
+    expect(of::max_abs_diff(cs, c) <= 1e-6f, "matmul_tile_strided_inplace", of::max_abs_diff(cs, c));
+
+    // error contract
+    expect_throw<std::invalid_argument>([&] { of::standard_attention(q, k, std::vector<float>(3), shape, options); },
+                                        "V size mismatch throws invalid_argument");
+    expect_throw<std::invalid_argument>([&] {
+        auto o = options;
+        o.key_block_size = 0;
+        of::flash_attention_tiled(q, k, v, shape, o);
+    }, "key_block_size 0 throws invalid_argument");
+    expect_throw<std::invalid_argument>([&] {
+        of::BlockMask bad = bm;
+        bad.allowed.pop_back();
+        auto o = options;
+        o.block_mask = &bad;
+        of::standard_attention(q, k, v, shape, o);
+    }, "bad BlockMask throws invalid_argument");
+    expect_throw<std::runtime_error>([&] {
+        of::run_attention(of::AttentionBackendKind::FlashMfmaHip, sin_values(128 * 96, 0.f), sin_values(128 * 96, 1.f),
+                          sin_values(128 * 96, 2.f), of::AttentionShape{128, 128, 96, 96}, options);
+    }, "unsupported MFMA shape throws runtime_error");
+
+    std::printf("%s\n", failures == 0 ? "ALL OK" : "FAILURES");
+    return failures == 0 ? 0 : 1;
+}

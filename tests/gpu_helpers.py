@@ -1,0 +1,61 @@
+"""Shared helpers of the GPU parity tests: seeded inputs rounded to the device
+dtype (the oracle gets their exact fp32 upcast), device upload, and the
+normwise error used as the pass criterion:
+
+    err = max|o - r| / max|r|   (fp32 <= 1e-4, bf16/fp16 <= 2e-2; max|o - r| reported)
+"""
+
+from __future__ import annotations
+
+import math
+import os
+
+import numpy as np
+
+from oracle import oracle as O
+
+TOL = {"f32": 1e-4, "bf16": 2e-2, "f16": 2e-2}
+THREADS = min(16, os.cpu_count() or 1)
+
+
+def torch_dtype(dt: str):
+    import torch
+    return {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[dt]
+
+
+def to_device(x32: np.ndarray, dt: str):
+    """Rounds to dt (RNE), uploads; returns (device tensor, fp32 upcast of the rounded values)."""
+    import torch
+    bits, up = O.round_to(x32, dt)
+    if dt == "f32":
+        t = torch.from_numpy(np.ascontiguousarray(bits)).cuda()
+    else:
+        t = torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).cuda().view(torch_dtype(dt))
+    return t, up
+
+
+def make_inputs(dt: str, B: int, H: int, M: int, N: int, D: int, Dv: int | None = None,
+                seed: int = 0, std: float = 1.0):
+    Dv = D if Dv is None else Dv
+    q = O.normal(3 * seed + 1, (B, H, M, D), std=std, threads=THREADS)
+    k = O.normal(3 * seed + 2, (B, H, N, D), std=std, threads=THREADS)
+    v = O.normal(3 * seed + 3, (B, H, N, Dv), std=std, threads=THREADS)
+    tq, uq = to_device(q, dt)
+    tk, uk = to_device(k, dt)
+    tv, uv = to_device(v, dt)
+    return (tq, tk, tv), (uq, uk, uv)
+
+
+def norm_error(out: np.ndarray, ref: np.ndarray) -> tuple[float, float]:
+    diff = np.abs(out.astype(np.float64) - ref.astype(np.float64))
+    maxabs = float(diff.max()) if diff.size else 0.0
+    denom = float(np.abs(ref).max()) if ref.size else 0.0
+    return (maxabs / denom if denom > 0 else maxabs), maxabs
+
+
+def alibi_slopes(H: int) -> np.ndarray:
+    return np.array([2.0 ** (-8.0 * (h + 1) / H) for h in range(H)], np.float32)
+
+
+def default_scale(D: int) -> float:
+    return 1.0 / math.sqrt(D)

@@ -1,0 +1,150 @@
+"""C ABI host-side checks (no GPU needed): the library loads, exports every
+entry point that include/onednn_flash_hip.h declares, validates arguments with
+the reference's error texts, and reports launch plans and useful FLOPs."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "onednn_flash_hip.h"
+
+
+def declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"^\s*(?:int|void|const char\*)\s+(ofh_\w+)\s*\(", text, re.M))
+
+
+def test_header_declarations_are_bound(ofh):
+    assert declared_functions() == set(ofh.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(ofh):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(ofh.LIB_PATH)], check=True,
+                         capture_output=True, text=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    missing = declared_functions() - exported
+    assert not missing, f"not exported: {missing}"
+    # and they resolve through ctypes
+    for name in declared_functions():
+        assert getattr(ofh.lib(), name) is not None
+
+
+def test_cpp_api_symbols_exported(ofh):
+    out = subprocess.run(["nm", "-DC", "--defined-only", str(ofh.LIB_PATH)], check=True,
+                         capture_output=True, text=True).stdout
+    for sym in ("onednn_flash::standard_attention(", "onednn_flash::flash_attention_tiled(",
+                "onednn_flash::flash_attention_q_tile(", "onednn_flash::flash_attention_qk_pv_tile(",
+                "onednn_flash::flash_attention_qk_pv_tile_ws(",
+                "onednn_flash::flash_attention_batched_qk_pv_tile(",
+                "onednn_flash::flash_attention_batched_device(", "onednn_flash::run_attention(",
+                "onednn_flash::backend_name(", "onednn_flash::max_abs_diff(",
+                "onednn_flash::BlockMask::allows(", "onednn_flash::matmul_tile(",
+                "onednn_flash::matmul_tile_inplace(", "onednn_flash::matmul_tile_strided_inplace(",
+                "onednn_flash::matmul_tile_reference(", "onednn_flash::matmul_tile_reference_inplace(",
+                "onednn_flash::tile_kernel_name(", "onednn_flash::AttentionWorkspace::resize("):
+        assert sym in out, sym
+
+
+def test_struct_layout_matches(ofh):
+    p = ofh.AttentionParams()
+    ofh.lib().ofh_attention_params_init(ctypes.byref(p))
+    assert p.struct_size == ctypes.sizeof(ofh.AttentionParams)
+    assert p.scale == 1.0 and p.dtype == ofh.DTYPE_F32 and p.algorithm == ofh.ALGO_AUTO
+    assert ofh.lib().ofh_abi_version() == 1
+
+
+def _expect_error(ofh, p, code, text):
+    with pytest.raises(ofh.OfhError) as e:
+        ofh.launch_info(p)
+    assert e.value.code == code
+    assert text in str(e.value)
+
+
+def test_validation_messages(ofh):
+    F = ofh
+    _expect_error(F, F.make_params(1, 1, 0, 4, 64), F.OFH_ERROR_INVALID_ARGUMENT,
+                  "batched attention dimensions must be non-zero")
+    _expect_error(F, F.make_params(1, 1, 4, 4, 64, mask_allowed=16, mask_query_block_size=0,
+                                   mask_key_block_size=1, mask_query_blocks=1, mask_key_blocks=1),
+                  F.OFH_ERROR_INVALID_ARGUMENT, "BlockMask block sizes must be non-zero")
+    _expect_error(F, F.make_params(1, 1, 4, 4, 64, mask_allowed=16, mask_query_block_size=1,
+                                   mask_key_block_size=1, mask_query_blocks=0, mask_key_blocks=1),
+                  F.OFH_ERROR_INVALID_ARGUMENT, "BlockMask dimensions must be non-zero")
+    p = F.make_params(1, 1, 4, 4, 64)
+    p.dtype = 7
+    _expect_error(F, p, F.OFH_ERROR_INVALID_ARGUMENT, "unknown dtype")
+    _expect_error(F, F.make_params(1, 1, 4, 4, 64, dtype=F.DTYPE_BF16, out_dtype=F.DTYPE_F16),
+                  F.OFH_ERROR_INVALID_ARGUMENT, "out_dtype")
+    _expect_error(F, F.make_params(1, 1, 4, 4, 64, softcap=-1.0), F.OFH_ERROR_INVALID_ARGUMENT,
+                  "softcap")
+    _expect_error(F, F.make_params(1, 1, 4, 4, 64, bias_kind=F.BIAS_ALIBI),
+                  F.OFH_ERROR_INVALID_ARGUMENT, "slopes")
+    _expect_error(F, F.make_params(1, 1, 4, 4, 96, algorithm=F.ALGO_FLASH_MFMA),
+                  F.OFH_ERROR_UNSUPPORTED, "flash MFMA kernel needs")
+    p = F.make_params(1, 1, 4, 4, 64)
+    p.struct_size = 8
+    _expect_error(F, p, F.OFH_ERROR_INVALID_ARGUMENT, "struct_size")
+
+
+def test_null_pointers_rejected_before_any_device_work(ofh):
+    F = ofh
+    p = F.make_params(1, 1, 4, 4, 64)
+    rc = F.lib().ofh_attention_fwd(ctypes.byref(p), None, None, None, None, None, 0, None)
+    assert rc == F.OFH_ERROR_INVALID_ARGUMENT
+    assert "pointers must be non-null" in F.lib().ofh_last_error().decode()
+
+
+def test_kernel_choice(ofh):
+    F = ofh
+    cases = [
+        (dict(dtype=F.DTYPE_BF16, head_dim=128), "flash_fwd_mfma16_kernel<bf16,128,plain>"),
+        (dict(dtype=F.DTYPE_F16, head_dim=64), "flash_fwd_mfma16_kernel<f16,64,plain>"),
+        (dict(dtype=F.DTYPE_F32, head_dim=64), "flash_fwd_mfma32_kernel<64,plain>"),
+        (dict(dtype=F.DTYPE_BF16, head_dim=128, softcap=50.0),
+         "flash_fwd_mfma16_kernel<bf16,128,general>"),
+        (dict(dtype=F.DTYPE_BF16, head_dim=96), "rowwise_fwd_kernel"),
+        (dict(dtype=F.DTYPE_BF16, head_dim=64, value_dim=128), "rowwise_fwd_kernel"),
+        (dict(dtype=F.DTYPE_F32, head_dim=64, algorithm=F.ALGO_ROWWISE), "rowwise_fwd_kernel"),
+    ]
+    for kw, name in cases:
+        D = kw.pop("head_dim")
+        Dv = kw.pop("value_dim", D)
+        info = F.launch_info(F.make_params(2, 3, 300, 200, D, Dv, **kw))
+        assert info.kernel_name.decode() == name
+    info = F.launch_info(F.make_params(4, 32, 4096, 4096, 128, dtype=F.DTYPE_BF16, causal=True))
+    assert info.workgroups == 4 * 32 * 32 and info.block_m == 128 and info.threads == 256
+
+
+def test_useful_flops_match_workloads(ofh):
+    import onednn_flash_configs as C
+    F = ofh
+    for w in C.WORKLOADS.values():
+        kw = {}
+        m = w.mask()
+        if m is not None:
+            kw = dict(mask_allowed=m.ctypes.data, mask_query_block_size=64, mask_key_block_size=64,
+                      mask_query_blocks=m.shape[0], mask_key_blocks=m.shape[1])
+        p = F.make_params(w.batch, w.heads, w.tokens, w.tokens, w.head_dim, causal=w.causal, **kw)
+        assert F.useful_flops(p) == w.useful_flops(), w.name
+    # BASELINE table values
+    assert C.get("c3").useful_flops() == 549_890_031_616
+    assert C.get("c5").useful_pairs_per_head() == 19_677_184
+    assert int(C.get("c5").mask().sum()) == 4930
+
+
+def test_workspace_bytes(ofh):
+    F = ofh
+    assert F.workspace_bytes(F.make_params(1, 1, 512, 512, 64, dtype=F.DTYPE_BF16)) == 0
+    m = np.ones((8, 8), np.uint8)
+    p = F.make_params(1, 1, 512, 512, 64, dtype=F.DTYPE_BF16, mask_allowed=m.ctypes.data,
+                      mask_query_block_size=64, mask_key_block_size=64, mask_query_blocks=8,
+                      mask_key_blocks=8)
+    nqt, nkt = 4, 8
+    assert F.workspace_bytes(p) == 256 + nqt * nkt * 4

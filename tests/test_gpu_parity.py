@@ -1,0 +1,257 @@
+"""GPU parity: the HIP kernels, called through the C ABI, against the oracle on
+the same seeded, identically rounded inputs.
+
+Small shapes are checked in full; the five benchmark workloads are checked at
+full size on sampled (head, row) pairs (rows are independent, so a sampled
+row of the oracle is exact). Pass criterion: normwise max|o-r|/max|r| <= 1e-4
+(fp32) / 2e-2 (bf16, fp16), with the max-abs error printed.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+
+from gpu_helpers import TOL, THREADS, alibi_slopes, make_inputs, norm_error, to_device
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+def run(F, dev, *, dt, causal=False, scale=None, mask=None, mbs=(1, 1), slopes=None, bias=None,
+        softcap=0.0, out_dtype="f32", algorithm=0, **kw):
+    tq, tk, tv = dev
+    D = tq.shape[3]
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    args = {}
+    if mask is not None:
+        args.update(mask=torch.from_numpy(np.ascontiguousarray(mask)).cuda(), mask_block_size=mbs)
+    if slopes is not None:
+        args["alibi_slopes"] = torch.from_numpy(slopes).cuda()
+    if bias is not None:
+        args["bias"] = torch.from_numpy(np.ascontiguousarray(bias)).cuda()
+    od = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[out_dtype]
+    out = F.attention_fwd(tq, tk, tv, scale=scale, causal=causal, softcap=softcap, out_dtype=od,
+                          algorithm=algorithm, **args, **kw)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def oracle_full(host, *, causal=False, scale=None, mask=None, mbs=(1, 1), slopes=None, bias=None,
+                softcap=0.0):
+    uq, uk, uv = host
+    B, H, M, D = uq.shape
+    N, Dv = uk.shape[2], uv.shape[3]
+    prob = O.Problem(B, H, M, N, D, Dv, scale=1.0 / math.sqrt(D) if scale is None else scale,
+                     causal=causal, mask=mask, mask_query_block_size=mbs[0],
+                     mask_key_block_size=mbs[1], alibi_slopes=slopes, dense_bias=bias,
+                     softcap=softcap)
+    return O.standard_attention(uq, uk, uv, prob)
+
+
+def check(out, ref, dt, label):
+    err, maxabs = norm_error(out, ref)
+    print(f"{label}: normwise {err:.3e} max-abs {maxabs:.3e} (tol {TOL[dt]:g})")
+    assert np.isfinite(out).all(), f"{label}: non-finite output"
+    assert err <= TOL[dt], f"{label}: normwise error {err:.3e} > {TOL[dt]:g}"
+    return err
+
+
+# ---------------------------------------------------------------------------
+# small shapes, full oracle
+
+SHAPES = [(1, 1), (7, 13), (64, 64), (128, 128), (200, 333), (333, 200)]
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_mfma_shapes(ofh, dt, D, causal):
+    for i, (M, N) in enumerate(SHAPES):
+        dev, host = make_inputs(dt, 2, 3, M, N, D, seed=i)
+        out = run(ofh, dev, dt=dt, causal=causal)
+        ref = oracle_full(host, causal=causal)
+        check(out, ref, dt, f"{dt} D{D} causal={causal} M{M} N{N}")
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_score_mods(ofh, dt):
+    B, H, M, N, D = 2, 4, 190, 257, 128 if dt != "f16" else 64
+    dev, host = make_inputs(dt, B, H, M, N, D, seed=7)
+    slopes = alibi_slopes(H)
+    for causal in (False, True):
+        for kw in (dict(slopes=slopes), dict(softcap=50.0), dict(slopes=slopes, softcap=50.0),
+                   dict(slopes=slopes, softcap=2.0)):
+            out = run(ofh, dev, dt=dt, causal=causal, **kw)
+            ref = oracle_full(host, causal=causal, **kw)
+            check(out, ref, dt, f"{dt} mods {sorted(kw)} causal={causal}")
+    bias = O.normal(99, (M, N), std=2.0)
+    out = run(ofh, dev, dt=dt, bias=bias, softcap=30.0)
+    check(out, oracle_full(host, bias=bias, softcap=30.0), dt, f"{dt} dense bias")
+
+
+def test_dense_bias_per_head(ofh):
+    B, H, M, N, D = 2, 3, 70, 90, 64
+    dev, host = make_inputs("bf16", B, H, M, N, D, seed=8)
+    bias = O.normal(5, (B, H, M, N), std=1.0)
+    out = run(ofh, dev, dt="bf16", bias=bias, causal=True)
+    uq, uk, uv = host
+    ref = np.zeros_like(out)
+    for b in range(B):
+        for h in range(H):
+            sl = (slice(b, b + 1), slice(h, h + 1))
+            ref[b, h] = oracle_full((uq[sl], uk[sl], uv[sl]), causal=True, bias=bias[b, h])[0, 0]
+    check(out, ref, "bf16", "per-head dense bias")
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_block_masks(ofh, dt):
+    rng = np.random.default_rng(3)
+    M, N, D = 300, 350, 64
+    dev, host = make_inputs(dt, 1, 2, M, N, D, seed=11)
+    for mbs in [(64, 64), (16, 32), (100, 7), (1, 1), (128, 64)]:
+        qb, kb = -(-M // mbs[0]), -(-N // mbs[1])
+        mask = (rng.random((qb, kb)) < 0.4).astype(np.uint8)
+        for causal in (False, True):
+            out = run(ofh, dev, dt=dt, causal=causal, mask=mask, mbs=mbs)
+            ref = oracle_full(host, causal=causal, mask=mask, mbs=mbs)
+            check(out, ref, dt, f"{dt} mask {mbs} causal={causal}")
+
+
+def test_fully_masked_rows_are_zero(ofh):
+    M, N, D = 256, 256, 128
+    dev, host = make_inputs("bf16", 1, 2, M, N, D, seed=12)
+    mask = np.ones((4, 4), np.uint8)
+    mask[1, :] = 0  # query rows 64..127 see nothing
+    mask = mask[:3]  # rows >= 192 are out of the bitmap's range: disallowed
+    out = run(ofh, dev, dt="bf16", mask=mask, mbs=(64, 64))
+    assert np.all(out[:, :, 64:128] == 0) and np.all(out[:, :, 192:] == 0)
+    check(out, oracle_full(host, mask=mask, mbs=(64, 64)), "bf16", "fully masked rows")
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_rowwise_kernel_any_shape(ofh, dt):
+    for M, N, D, Dv, causal in [(33, 47, 16, 16, True), (40, 70, 96, 96, False),
+                                (20, 30, 64, 128, True), (9, 600, 200, 40, False)]:
+        dev, host = make_inputs(dt, 1, 2, M, N, D, Dv, seed=M)
+        slopes = alibi_slopes(2)
+        out = run(ofh, dev, dt=dt, causal=causal, slopes=slopes, softcap=20.0)
+        ref = oracle_full(host, causal=causal, slopes=slopes, softcap=20.0)
+        check(out, ref, dt, f"{dt} rowwise M{M} N{N} D{D} Dv{Dv}")
+    # the explicit rowwise algorithm on an MFMA-capable shape
+    dev, host = make_inputs(dt, 1, 2, 100, 120, 64, seed=1)
+    out = run(ofh, dev, dt=dt, causal=True, algorithm=ofh.ALGO_ROWWISE)
+    check(out, oracle_full(host, causal=True), dt, f"{dt} rowwise forced")
+
+
+def test_strided_layouts(ofh):
+    B, H, M, N, D = 2, 4, 150, 170, 128
+    dev, host = make_inputs("bf16", B, H, M, N, D, seed=13)
+    # [B,T,H,D] storage viewed as [B,H,T,D]
+    tq, tk, tv = (t.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3) for t in dev)
+    out_store = torch.empty((B, M, H, D), device="cuda", dtype=torch.float32)
+    out = out_store.permute(0, 2, 1, 3)
+    ofh.attention_fwd(tq, tk, tv, causal=True, out=out)
+    torch.cuda.synchronize()
+    check(out.cpu().numpy(), oracle_full(host, causal=True), "bf16", "strided [B,T,H,D]")
+
+
+def test_output_dtypes_and_determinism(ofh):
+    dev, host = make_inputs("bf16", 1, 4, 256, 256, 128, seed=14)
+    a = run(ofh, dev, dt="bf16", causal=True, out_dtype="bf16")
+    b = run(ofh, dev, dt="bf16", causal=True, out_dtype="f32")
+    c = run(ofh, dev, dt="bf16", causal=True, out_dtype="f32")
+    assert np.array_equal(b, c), "not deterministic"
+    # the bf16 output is the fp32 output rounded to nearest even
+    np.testing.assert_array_equal(a, O.bf16_bits_to_f32(O.f32_to_bf16_bits(b)))
+    check(a, oracle_full(host, causal=True), "bf16", "bf16 output")
+
+
+def test_explicit_workspace(ofh):
+    F = ofh
+    M = N = 512
+    dev, host = make_inputs("f16", 1, 2, M, N, 64, seed=15)
+    mask = np.tril(np.ones((8, 8), np.uint8))
+    tmask = torch.from_numpy(mask).cuda()
+    p = F.make_params(1, 2, M, N, 64, dtype=F.DTYPE_F16, mask_allowed=tmask.data_ptr(),
+                      mask_query_block_size=64, mask_key_block_size=64, mask_query_blocks=8,
+                      mask_key_blocks=8)
+    need = F.workspace_bytes(p)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    out = F.attention_fwd(*dev, causal=False, mask=tmask, mask_block_size=(64, 64), workspace=ws,
+                          out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    check(out.cpu().numpy(), oracle_full(host, mask=mask, mbs=(64, 64)), "f16", "explicit workspace")
+    small = torch.empty(need - 4, dtype=torch.uint8, device="cuda")
+    with pytest.raises(F.OfhError) as e:
+        F.attention_fwd(*dev, mask=tmask, mask_block_size=(64, 64), workspace=small)
+    assert e.value.code == F.OFH_ERROR_WORKSPACE_TOO_SMALL
+
+
+def test_host_entry_point(ofh):
+    F = ofh
+    B, H, M, N, D = 1, 2, 100, 130, 64
+    q, k, v = (O.normal(s, shp) for s, shp in ((1, (B, H, M, D)), (2, (B, H, N, D)), (3, (B, H, N, D))))
+    for dt, code in (("f32", F.DTYPE_F32), ("bf16", F.DTYPE_BF16)):
+        out = np.zeros((B, H, M, D), np.float32)
+        slopes = alibi_slopes(H)
+        p = F.make_params(B, H, M, N, D, dtype=code, out_dtype=F.DTYPE_F32, scale=0.125,
+                          causal=True, bias_kind=F.BIAS_ALIBI, alibi_slopes=slopes.ctypes.data)
+        F.check(F.lib().ofh_attention_fwd_host(ctypes.byref(p), q.ctypes.data, k.ctypes.data,
+                                               v.ctypes.data, out.ctypes.data))
+        host = tuple(O.round_to(x, dt)[1] for x in (q, k, v))
+        ref = oracle_full(host, causal=True, scale=0.125, slopes=slopes)
+        check(out, ref, dt, f"host entry {dt}")
+
+
+# ---------------------------------------------------------------------------
+# the five workloads at full size, sampled rows
+
+def _sampled_check(F, w, rows_per_head=48, heads=8, seed=100):
+    dev, host = make_inputs(w.dtype, w.batch, w.heads, w.tokens, w.tokens, w.head_dim, seed=seed,
+                            std=w.std)
+    mask = w.mask()
+    slopes = w.alibi_slopes() if w.alibi else None
+    out = run(F, dev, dt=w.dtype, causal=w.causal, scale=w.scale, mask=mask, mbs=(64, 64),
+              slopes=slopes, softcap=w.softcap, out_dtype=w.dtype)
+    BH = w.batch * w.heads
+    rng = np.random.default_rng(seed)
+    hsel = rng.choice(BH, size=min(heads, BH), replace=False)
+    head_idx, rows = [], []
+    for h in hsel:
+        r = rng.choice(w.tokens, size=rows_per_head - 2, replace=False)
+        r = np.concatenate([r, [0, w.tokens - 1]])  # first and last row always
+        head_idx += [h] * len(r)
+        rows += list(r)
+    head_idx, rows = np.array(head_idx), np.array(rows)
+    uq, uk, uv = host
+    prob = O.Problem(w.batch, w.heads, w.tokens, w.tokens, w.head_dim, w.head_dim, scale=w.scale,
+                     causal=w.causal, mask=mask, mask_query_block_size=64, mask_key_block_size=64,
+                     alibi_slopes=slopes, softcap=w.softcap)
+    ref = O.standard_attention_rows(uq, uk, uv, prob, head_idx, rows, threads=THREADS)
+    got = out.reshape(BH, w.tokens, w.head_dim)[head_idx, rows]
+    check(got, ref, w.dtype, f"{w.name} ({len(rows)} sampled rows)")
+    assert np.isfinite(out).all()
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4", "c5"])
+def test_workload_full_size(ofh, name):
+    import onednn_flash_configs as C
+    w = C.get(name)
+    if name in ("c1", "c2"):
+        # small enough for every row
+        _sampled_check(ofh, w, rows_per_head=w.tokens, heads=w.batch * w.heads)
+    else:
+        _sampled_check(ofh, w)
