@@ -40,7 +40,7 @@ struct Resolved {
     int algorithm;       // OFH_ALGO_FLASH_MFMA or OFH_ALGO_ROWWISE
     bool general_mod;    // bias or soft-cap present
     bool tile_list;      // block-mask tile lists are built
-    int block_n;
+    int block_m, block_n, threads;
     int num_q_tiles, num_k_tiles;
 };
 
@@ -148,14 +148,19 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
         if (p->head_dim > 1024)
             return set_error(OFH_ERROR_UNSUPPORTED, "rowwise kernel supports head_dim <= 1024");
         r.tile_list = false;
-        r.block_n = 0;
+        r.block_m = 1;
+        r.block_n = 64;
+        r.threads = 256;
         r.num_q_tiles = 0;
         r.num_k_tiles = 0;
         return OFH_SUCCESS;
     }
     r.algorithm = OFH_ALGO_FLASH_MFMA;
-    r.block_n = ofh::flash_mfma_block_n(p->dtype);
-    r.num_q_tiles = (int)((p->query_tokens + ofh::kBlockM - 1) / ofh::kBlockM);
+    const ofh::MfmaTiles tiles = ofh::flash_mfma_tiles(p->dtype);
+    r.block_m = tiles.block_m;
+    r.block_n = tiles.block_n;
+    r.threads = tiles.threads;
+    r.num_q_tiles = (int)((p->query_tokens + r.block_m - 1) / r.block_m);
     r.num_k_tiles = (int)((p->key_tokens + r.block_n - 1) / r.block_n);
     r.tile_list = p->mask_allowed != nullptr;
     const int64_t grid = (int64_t)p->batch * p->heads * r.num_q_tiles;
@@ -265,7 +270,7 @@ int fwd_impl(const ofh_attention_params* p, const void* q, const void* k, const 
         ofh::TileListArgs t;
         t.M = a.M;
         t.N = a.N;
-        t.block_m = ofh::kBlockM;
+        t.block_m = r.block_m;
         t.block_n = r.block_n;
         t.causal = a.causal;
         t.mask = a.mask;
@@ -433,9 +438,9 @@ int ofh_attention_launch_info(const ofh_attention_params* p, ofh_launch_info* in
     info->uses_tile_list = r.tile_list ? 1 : 0;
     const char* name;
     if (r.algorithm == OFH_ALGO_FLASH_MFMA) {
-        info->block_m = ofh::kBlockM;
+        info->block_m = r.block_m;
         info->block_n = r.block_n;
-        info->threads = ofh::kThreads;
+        info->threads = r.threads;
         info->workgroups = (int64_t)p->batch * p->heads * r.num_q_tiles;
         name = ofh::flash_mfma_kernel_name(p->dtype, (int)p->head_dim, r.general_mod);
     } else {

@@ -171,26 +171,86 @@ __device__ __forceinline__ float online_softmax_tile(const FwdArgs& a, f32x16 (&
 
 // ---------------------------------------------------------------------------
 // bf16 / fp16 inputs, fp32 accumulate: v_mfma_f32_32x32x16_{bf16,f16}.
+//
+// 8 wavefronts x 32 query rows = 256 queries per workgroup, 2 wavefronts per
+// SIMD so that one wavefront's softmax (VALU) overlaps the other's MFMAs.
+// K/V tiles of 64 keys are staged global -> registers -> LDS one tile ahead,
+// double-buffered, one barrier per tile. Loads are unconditional (rows past
+// the end are clamped to the last row, their V values zeroed, their scores
+// masked), so no exec-masked branches break the compiler's wait counting.
+//
+// LDS layout: both tiles row-major [key][d] with the 16-byte chunk index of
+// each row XOR-swizzled. The K swizzle makes the A-operand reads (16 rows
+// kappa(0..15) at one chunk column per 16 lanes) hit 16 distinct bank quads;
+// the V swizzle makes the ds_read_b64_tr_b16 reads (rows {0..3} x 4 chunk
+// columns per instruction half) hit distinct bank quads. The transposed read
+// delivers V^T fragments directly, so V is never transposed in a separate
+// pass.
+//
+// Online softmax with lazy rescaling: the running max m that probabilities
+// are taken against is raised only when a tile's max exceeds it by more than
+// kRescaleSlack (log2 units), so p <= 2^8 and the O/l rescale (a wave-uniform
+// branch) runs on a few tiles per row instead of every tile. The result is
+// exact in real arithmetic: O and l share the same stale max.
+
+constexpr int kWaves16 = 8;
+constexpr int kThreads16 = kWaves16 * 64;
+constexpr int kBlockM16 = kWaves16 * kQueriesPerWave;  // 256
+constexpr int kBlockN16 = 64;
+constexpr float kRescaleSlack = 8.0f;
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+typedef __attribute__((address_space(3))) unsigned char lds_u8;
+
+template <int D>
+struct TileLayout {
+    static constexpr int RB = D * 2;             // bytes per K/V row
+    static constexpr int CPR = D / 8;            // 16-byte chunks per row
+    static constexpr int TILE = kBlockN16 * RB;  // bytes of one K (or V) tile
+    static __device__ __forceinline__ int kswz(int row) { return D == 128 ? (row & 15) : ((row >> 1) & 7); }
+    static __device__ __forceinline__ int vswz(int row) {
+        return D == 128 ? ((row & 3) << 2) : (((row >> 1) & 1) << 2);
+    }
+    static __device__ __forceinline__ int kaddr(int row, int chunk) { return row * RB + ((chunk ^ kswz(row)) << 4); }
+    static __device__ __forceinline__ int vaddr(int row, int chunk) { return row * RB + ((chunk ^ vswz(row)) << 4); }
+};
+
+// max over both 32-lane halves (lane l and l^32 hold the same query row)
+__device__ __forceinline__ float half_swap_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x),
+                                                    __builtin_bit_cast(unsigned, x), false, false);
+    return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
+
+template <typename T>
+struct Dot2;
+template <>
+struct Dot2<__bf16> {
+    typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+    static __device__ __forceinline__ float sum2(v2 a, float acc) {
+        return __builtin_amdgcn_fdot2_f32_bf16(a, v2{(__bf16)1.0f, (__bf16)1.0f}, acc, false);
+    }
+};
+template <>
+struct Dot2<_Float16> {
+    typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+    static __device__ __forceinline__ float sum2(v2 a, float acc) {
+        return __builtin_amdgcn_fdot2(a, v2{(_Float16)1.0f, (_Float16)1.0f}, acc, false);
+    }
+};
 
 template <typename T, int D, bool GENERAL>
-__global__ __launch_bounds__(kThreads) void flash_fwd_mfma16_kernel(FwdArgs a) {
+__global__ __launch_bounds__(kThreads16) void flash_fwd_mfma16_kernel(FwdArgs a) {
     using M16 = Mfma16<T>;
     using v8 = typename M16::v8;
-    constexpr int BN = kBlockN;
-    constexpr int KSTR = D + 8;   // K tile row stride in LDS (elements): 16-byte pad
-    constexpr int VSTR = BN + 8;  // V^T tile row stride in LDS (elements)
-    constexpr int KTILE = BN * KSTR;
-    constexpr int VTILE = D * VSTR;
-    constexpr int STAGE = KTILE + VTILE;
-    constexpr int CHUNKS = BN * D / 8;        // 16-byte chunks per K (or V) tile
-    constexpr int CPT = CHUNKS / kThreads;    // chunks per thread
-    constexpr int NDC = D / 8;                // 16-byte chunks per row
-    constexpr int NKG = BN / CPT;             // key groups of the V transposition
-    static_assert(CHUNKS % kThreads == 0, "tile must split evenly over the workgroup");
-    static_assert(CPT == 2 || CPT == 4, "V transposition handles 2 or 4 keys per thread");
-    static_assert(NKG * NDC == kThreads, "V transposition covers the tile");
+    using L = TileLayout<D>;
+    constexpr int BN = kBlockN16;
+    constexpr int CPT = BN * L::CPR / kThreads16;  // 16-byte chunks per thread per tile
+    static_assert(CPT >= 1 && BN * L::CPR % kThreads16 == 0, "tile must split evenly");
 
-    __shared__ __attribute__((aligned(16))) unsigned short lds[2 * STAGE];
+    __shared__ __attribute__((aligned(16))) unsigned char smem[4 * L::TILE];  // K0 V0 K1 V1
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 5, r = lane & 31;
@@ -201,20 +261,16 @@ __global__ __launch_bounds__(kThreads) void flash_fwd_mfma16_kernel(FwdArgs a) {
     const T* __restrict__ Qp = (const T*)a.q + b * a.q_sb + h * a.q_sh;
     const T* __restrict__ Kp = (const T*)a.k + b * a.k_sb + h * a.k_sh;
     const T* __restrict__ Vp = (const T*)a.v + b * a.v_sb + h * a.v_sh;
-    const int q0 = qt * kBlockM;
+    const int q0 = qt * kBlockM16;
     const int qw0 = q0 + wave * kQueriesPerWave;
     const int my_q = qw0 + r;
 
     // Q^T fragments (B operand of S^T = K Q^T): lane holds Q[my_q][16c + 8g .. +7].
     v8 qf[D / 16];
     {
-        const T* qrow = Qp + (int64_t)my_q * a.q_sm + 8 * g;
+        const T* qrow = Qp + (int64_t)min(my_q, a.M - 1) * a.q_sm + 8 * g;
 #pragma unroll
-        for (int c = 0; c < D / 16; ++c) {
-            u32x4 u = {0u, 0u, 0u, 0u};
-            if (my_q < a.M) u = *(const u32x4*)(qrow + 16 * c);
-            qf[c] = __builtin_bit_cast(v8, u);
-        }
+        for (int c = 0; c < D / 16; ++c) qf[c] = __builtin_bit_cast(v8, *(const u32x4*)(qrow + 16 * c));
     }
 
     int ntiles;
@@ -223,62 +279,9 @@ __global__ __launch_bounds__(kThreads) void flash_fwd_mfma16_kernel(FwdArgs a) {
         ntiles = a.tile_counts[qt];
         list = a.tile_entries + (int64_t)qt * a.num_k_tiles;
     } else {
-        const int kend = a.causal ? min(a.N, q0 + kBlockM) : a.N;
+        const int kend = a.causal ? min(a.N, q0 + kBlockM16) : a.N;
         ntiles = (kend + BN - 1) / BN;
     }
-
-    u32x4 kreg[CPT], vreg[CPT];
-    const int vkg = tid % NKG, vdc = tid / NKG;
-    auto load_tile = [&](int kt) {
-        const int k0 = kt * BN;
-#pragma unroll
-        for (int u = 0; u < CPT; ++u) {
-            const int ci = tid + kThreads * u;
-            const int row = ci / NDC, cc = ci % NDC;
-            const int kj = k0 + row;
-            kreg[u] = u32x4{0u, 0u, 0u, 0u};
-            if (kj < a.N) kreg[u] = *(const u32x4*)(Kp + (int64_t)kj * a.k_sn + 8 * cc);
-        }
-#pragma unroll
-        for (int u = 0; u < CPT; ++u) {
-            const int kj = k0 + vkg * CPT + u;
-            vreg[u] = u32x4{0u, 0u, 0u, 0u};
-            if (kj < a.N) vreg[u] = *(const u32x4*)(Vp + (int64_t)kj * a.v_sn + 8 * vdc);
-        }
-    };
-    auto store_tile = [&](int buf) {
-        unsigned short* Ks = lds + buf * STAGE;
-        unsigned short* Vs = Ks + KTILE;
-#pragma unroll
-        for (int u = 0; u < CPT; ++u) {
-            const int ci = tid + kThreads * u;
-            const int row = ci / NDC, cc = ci % NDC;
-            *(u32x4*)(Ks + row * KSTR + 8 * cc) = kreg[u];
-        }
-        // V^T: element e of this thread's 8-wide d chunk, CPT consecutive keys.
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int w = e >> 1;
-            unsigned short* dst = Vs + (8 * vdc + e) * VSTR + vkg * CPT;
-            if constexpr (CPT == 4) {
-                const unsigned x0 = vreg[0][w], x1 = vreg[1][w], x2 = vreg[2][w], x3 = vreg[3][w];
-                u32x2 val;
-                if (e & 1) {
-                    val[0] = (x0 >> 16) | (x1 & 0xffff0000u);
-                    val[1] = (x2 >> 16) | (x3 & 0xffff0000u);
-                } else {
-                    val[0] = (x0 & 0xffffu) | (x1 << 16);
-                    val[1] = (x2 & 0xffffu) | (x3 << 16);
-                }
-                *(u32x2*)dst = val;
-            } else {
-                const unsigned x0 = vreg[0][w], x1 = vreg[1][w];
-                const unsigned val = (e & 1) ? ((x0 >> 16) | (x1 & 0xffff0000u))
-                                             : ((x0 & 0xffffu) | (x1 << 16));
-                *(unsigned*)dst = val;
-            }
-        }
-    };
     auto tile_at = [&](int it, bool& partial) -> int {
         if (list != nullptr) {
             const int e = list[it];
@@ -289,6 +292,42 @@ __global__ __launch_bounds__(kThreads) void flash_fwd_mfma16_kernel(FwdArgs a) {
         return it;
     };
 
+    // Global -> register staging of one K/V tile; rows past N are clamped to N-1.
+    u32x4 kreg[CPT], vreg[CPT];
+    auto load_tile = [&](int kt) {
+        const int k0 = kt * BN;
+#pragma unroll
+        for (int u = 0; u < CPT; ++u) {
+            const int ci = tid + kThreads16 * u;
+            const int row = ci / L::CPR, c = ci % L::CPR;
+            const int kj = min(k0 + row, a.N - 1);
+            kreg[u] = *(const u32x4*)(Kp + (int64_t)kj * a.k_sn + 8 * c);
+            vreg[u] = *(const u32x4*)(Vp + (int64_t)kj * a.v_sn + 8 * c);
+        }
+    };
+    auto store_tile = [&](int buf, int kt) {
+        unsigned char* Kb = smem + buf * 2 * L::TILE;
+        unsigned char* Vb = Kb + L::TILE;
+        const int k0 = kt * BN;
+#pragma unroll
+        for (int u = 0; u < CPT; ++u) {
+            const int ci = tid + kThreads16 * u;
+            const int row = ci / L::CPR, c = ci % L::CPR;
+            *(u32x4*)(Kb + L::kaddr(row, c)) = kreg[u];
+            const u32x4 zero = {0u, 0u, 0u, 0u};
+            *(u32x4*)(Vb + L::vaddr(row, c)) = (k0 + row < a.N) ? vreg[u] : zero;
+        }
+    };
+
+    // Per-lane constants of the transposed V reads: input lane j of a 16-lane
+    // group reads key (j/4) of a 4-key group at d-chunk cmap(j%4) of the lane
+    // group's 16 columns; cmap = {0,2,1,3} applies kappa to the output rows.
+    const int G = lane >> 4, j = lane & 15;
+    const int v_key = 8 * g + (j >> 2);
+    const int v_dquad = 16 * (G & 1) + 4 * ((j & 1) * 2 + ((j >> 1) & 1));  // d offset within 32
+    // K A-operand row of this lane within a 32-key block
+    const int k_row = kappa(r);
+
     f32x16 o[D / 32];
 #pragma unroll
     for (int db = 0; db < D / 32; ++db) o[db] = f32x16{};
@@ -297,61 +336,132 @@ __global__ __launch_bounds__(kThreads) void flash_fwd_mfma16_kernel(FwdArgs a) {
     const float* bias_row = nullptr;
     if (GENERAL && a.bias_kind == BIAS_DENSE && my_q < a.M)
         bias_row = a.bias + b * a.bias_sb + h * a.bias_sh + (int64_t)my_q * a.bias_sm;
+    const bool wave_has_rows = qw0 < a.M;
 
     if (ntiles > 0) {
         bool p0;
-        load_tile(tile_at(0, p0));
-        store_tile(0);
+        const int kt0 = tile_at(0, p0);
+        load_tile(kt0);
+        store_tile(0, kt0);
     }
     __syncthreads();
 
     for (int it = 0; it < ntiles; ++it) {
         bool partial;
         const int kt = tile_at(it, partial);
+        int kt_next = 0;
         if (it + 1 < ntiles) {
             bool pn;
-            load_tile(tile_at(it + 1, pn));
+            kt_next = tile_at(it + 1, pn);
+            load_tile(kt_next);
         }
-        const unsigned short* Ks = lds + (it & 1) * STAGE;
-        const unsigned short* Vs = Ks + KTILE;
+        const unsigned char* Kb = smem + (it & 1) * 2 * L::TILE;
+        const unsigned char* Vb = Kb + L::TILE;
         const int k0 = kt * BN;
-        const bool active = !(a.causal && k0 > qw0 + kQueriesPerWave - 1);
+        const bool active = wave_has_rows && !(a.causal && k0 > qw0 + kQueriesPerWave - 1);
         if (active) {
             const bool need_mask = list != nullptr
                                        ? partial
                                        : ((k0 + BN > a.N) || (a.causal && k0 + BN - 1 > qw0));
+            // S^T = K Q^T for 64 keys: two 32x32 blocks.
             f32x16 s[BN / 32];
 #pragma unroll
             for (int sb = 0; sb < BN / 32; ++sb) {
                 s[sb] = f32x16{};
-                const unsigned short* krow = Ks + (32 * sb + kappa(r)) * KSTR + 8 * g;
+                const int row = 32 * sb + k_row;
 #pragma unroll
                 for (int c = 0; c < D / 16; ++c) {
-                    const v8 af = __builtin_bit_cast(v8, *(const u32x4*)(krow + 16 * c));
+                    const v8 af = __builtin_bit_cast(v8, *(const u32x4*)(Kb + L::kaddr(row, 2 * c + g)));
                     s[sb] = M16::mma(af, qf[c], s[sb]);
                 }
             }
-            const float alpha = online_softmax_tile<BN / 32, GENERAL>(
-                a, s, need_mask, my_q, k0, g, slope, bias_row, m_run, l_run);
+
+            // Scores in log2 units; masked entries -inf.
+            float mx = kNegInf;
+            if (!GENERAL && !need_mask) {
+                float smax = kNegInf, smin = __builtin_huge_valf();
 #pragma unroll
-            for (int db = 0; db < D / 32; ++db) o[db] *= alpha;
-            v8 pf[BN / 16];
+                for (int sb = 0; sb < BN / 32; ++sb)
 #pragma unroll
-            for (int c = 0; c < BN / 16; ++c) {
+                    for (int e = 0; e < 16; ++e) {
+                        smax = fmaxf(smax, s[sb][e]);
+                        smin = fminf(smin, s[sb][e]);
+                    }
+                mx = a.scale_log2 >= 0.0f ? smax * a.scale_log2 : smin * a.scale_log2;
+            } else {
+                const bool row_out = GENERAL && my_q >= a.M;
 #pragma unroll
-                for (int t = 0; t < 8; ++t) pf[c][t] = (T)s[c >> 1][8 * (c & 1) + t];
+                for (int sb = 0; sb < BN / 32; ++sb)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int kj = k0 + 32 * sb + acc_pos(e, g);
+                        const bool msk = row_out || (need_mask && elem_masked(a, my_q, kj));
+                        float x = kNegInf;
+                        if (!msk) {
+                            x = GENERAL ? general_score(a, s[sb][e], my_q, kj, slope, bias_row)
+                                        : s[sb][e] * a.scale_log2;
+                        }
+                        s[sb][e] = x;
+                        mx = fmaxf(mx, x);
+                    }
             }
+            mx = half_swap_max(mx);
+
+            // Lazy rescale (wave-uniform branch).
+            const bool raise = mx > m_run + kRescaleSlack;
+            if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+                // lanes that do not raise keep their max and scale by exactly 1
+                // (their m_run may be -inf: -inf - -inf must not reach exp2)
+                const float alpha = raise ? __builtin_amdgcn_exp2f(m_run - mx) : 1.0f;
+                m_run = raise ? mx : m_run;
+                l_run *= alpha;
+#pragma unroll
+                for (int db = 0; db < D / 32; ++db) o[db] *= alpha;
+            }
+            const float m_use = (m_run == kNegInf) ? 0.0f : m_run;
+
+            // Probabilities, packed to the MFMA input type; row sum from the packed values.
+            v8 pf[BN / 16];
+            if (!GENERAL && !need_mask) {
+#pragma unroll
+                for (int c = 0; c < BN / 16; ++c)
+#pragma unroll
+                    for (int t = 0; t < 8; ++t)
+                        pf[c][t] = (T)__builtin_amdgcn_exp2f(
+                            __builtin_fmaf(s[c >> 1][8 * (c & 1) + t], a.scale_log2, -m_use));
+            } else {
+#pragma unroll
+                for (int c = 0; c < BN / 16; ++c)
+#pragma unroll
+                    for (int t = 0; t < 8; ++t)
+                        pf[c][t] = (T)__builtin_amdgcn_exp2f(s[c >> 1][8 * (c & 1) + t] - m_use);
+            }
+            float lsum = 0.0f;
+#pragma unroll
+            for (int c = 0; c < BN / 16; ++c)
+#pragma unroll
+                for (int t = 0; t < 8; t += 2)
+                    lsum = Dot2<T>::sum2(typename Dot2<T>::v2{pf[c][t], pf[c][t + 1]}, lsum);
+            l_run += lsum;
+
+            // O^T += V^T P^T: A operand from two transposed 4-key reads.
 #pragma unroll
             for (int db = 0; db < D / 32; ++db) {
-                const unsigned short* vrow = Vs + (32 * db + kappa(r)) * VSTR + 8 * g;
+                const int d = 32 * db + v_dquad;
+                const int chunk = d >> 3, half = (d & 4) * 2;  // byte offset 0 or 8 in the chunk
 #pragma unroll
                 for (int c = 0; c < BN / 16; ++c) {
-                    const v8 af = __builtin_bit_cast(v8, *(const u32x4*)(vrow + 16 * c));
-                    o[db] = M16::mma(af, pf[c], o[db]);
+                    const int key = 16 * c + v_key;
+                    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_i16x4*)((lds_u8*)Vb + L::vaddr(key, chunk) + half));
+                    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_i16x4*)((lds_u8*)Vb + L::vaddr(key + 4, chunk) + half));
+                    const i16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                    o[db] = M16::mma(__builtin_bit_cast(v8, both), pf[c], o[db]);
                 }
             }
         }
-        if (it + 1 < ntiles) store_tile((it + 1) & 1);
+        if (it + 1 < ntiles) store_tile((it + 1) & 1, kt_next);
         __syncthreads();
     }
 
@@ -398,18 +508,21 @@ __global__ __launch_bounds__(kThreads) void flash_fwd_mfma16_kernel(FwdArgs a) {
 // and each PV step takes the two keys that the lane halves hold in register u.
 
 constexpr int kBlockNF32 = 32;
+constexpr int kWaves32 = 4;
+constexpr int kThreads32 = kWaves32 * 64;
+constexpr int kBlockM32 = kWaves32 * kQueriesPerWave;  // 128
 
 template <int D, bool GENERAL>
-__global__ __launch_bounds__(kThreads) void flash_fwd_mfma32_kernel(FwdArgs a) {
+__global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a) {
     constexpr int BN = kBlockNF32;
     constexpr int KSTR = D + 4;  // floats; conflict-free 16-byte reads of rows kappa(r)
     constexpr int VSTR = D + 4;  // floats; lane halves read rows 8 apart -> opposite bank halves
     constexpr int KTILE = BN * KSTR;
     constexpr int STAGE = 2 * KTILE;
     constexpr int CHUNKS = BN * D / 4;
-    constexpr int CPT = CHUNKS / kThreads;
+    constexpr int CPT = CHUNKS / kThreads32;
     constexpr int NDC = D / 4;
-    static_assert(CHUNKS % kThreads == 0, "tile must split evenly over the workgroup");
+    static_assert(CHUNKS % kThreads32 == 0, "tile must split evenly over the workgroup");
 
     __shared__ __attribute__((aligned(16))) float lds[2 * STAGE];
 
@@ -422,7 +535,7 @@ __global__ __launch_bounds__(kThreads) void flash_fwd_mfma32_kernel(FwdArgs a) {
     const float* __restrict__ Qp = (const float*)a.q + b * a.q_sb + h * a.q_sh;
     const float* __restrict__ Kp = (const float*)a.k + b * a.k_sb + h * a.k_sh;
     const float* __restrict__ Vp = (const float*)a.v + b * a.v_sb + h * a.v_sh;
-    const int q0 = qt * kBlockM;
+    const int q0 = qt * kBlockM32;
     const int qw0 = q0 + wave * kQueriesPerWave;
     const int my_q = qw0 + r;
 
@@ -444,7 +557,7 @@ __global__ __launch_bounds__(kThreads) void flash_fwd_mfma32_kernel(FwdArgs a) {
         ntiles = a.tile_counts[qt];
         list = a.tile_entries + (int64_t)qt * a.num_k_tiles;
     } else {
-        const int kend = a.causal ? min(a.N, q0 + kBlockM) : a.N;
+        const int kend = a.causal ? min(a.N, q0 + kBlockM32) : a.N;
         ntiles = (kend + BN - 1) / BN;
     }
 
@@ -453,7 +566,7 @@ __global__ __launch_bounds__(kThreads) void flash_fwd_mfma32_kernel(FwdArgs a) {
         const int k0 = kt * BN;
 #pragma unroll
         for (int u = 0; u < CPT; ++u) {
-            const int ci = tid + kThreads * u;
+            const int ci = tid + kThreads32 * u;
             const int row = ci / NDC, cc = ci % NDC;
             const int kj = k0 + row;
             kreg[u] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -469,7 +582,7 @@ __global__ __launch_bounds__(kThreads) void flash_fwd_mfma32_kernel(FwdArgs a) {
         float* Vs = Ks + KTILE;
 #pragma unroll
         for (int u = 0; u < CPT; ++u) {
-            const int ci = tid + kThreads * u;
+            const int ci = tid + kThreads32 * u;
             const int row = ci / NDC, cc = ci % NDC;
             *(f32x4*)(Ks + row * KSTR + 4 * cc) = kreg[u];
             *(f32x4*)(Vs + row * VSTR + 4 * cc) = vreg[u];
@@ -560,28 +673,28 @@ __global__ __launch_bounds__(kThreads) void flash_fwd_mfma32_kernel(FwdArgs a) {
 }
 
 template <typename K>
-hipError_t launch(K kernel, const FwdArgs& a, hipStream_t s) {
+hipError_t launch(K kernel, int threads, const FwdArgs& a, hipStream_t s) {
     const int64_t grid = (int64_t)a.B * a.H * a.num_q_tiles;
     if (grid <= 0) return hipSuccess;
-    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(threads), 0, s, a);
     return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipStream_t s) {
-#define OFH_DISPATCH_GM(KERNEL, ...)                                   \
-    return general_mod ? launch(KERNEL<__VA_ARGS__, true>, a, s)        \
-                       : launch(KERNEL<__VA_ARGS__, false>, a, s)
+#define OFH_DISPATCH_GM(KERNEL, THREADS, ...)                                   \
+    return general_mod ? launch(KERNEL<__VA_ARGS__, true>, THREADS, a, s)        \
+                       : launch(KERNEL<__VA_ARGS__, false>, THREADS, a, s)
     if (dtype == DT_BF16) {
-        if (a.D == 64) { OFH_DISPATCH_GM(flash_fwd_mfma16_kernel, __bf16, 64); }
-        if (a.D == 128) { OFH_DISPATCH_GM(flash_fwd_mfma16_kernel, __bf16, 128); }
+        if (a.D == 64) { OFH_DISPATCH_GM(flash_fwd_mfma16_kernel, kThreads16, __bf16, 64); }
+        if (a.D == 128) { OFH_DISPATCH_GM(flash_fwd_mfma16_kernel, kThreads16, __bf16, 128); }
     } else if (dtype == DT_F16) {
-        if (a.D == 64) { OFH_DISPATCH_GM(flash_fwd_mfma16_kernel, _Float16, 64); }
-        if (a.D == 128) { OFH_DISPATCH_GM(flash_fwd_mfma16_kernel, _Float16, 128); }
+        if (a.D == 64) { OFH_DISPATCH_GM(flash_fwd_mfma16_kernel, kThreads16, _Float16, 64); }
+        if (a.D == 128) { OFH_DISPATCH_GM(flash_fwd_mfma16_kernel, kThreads16, _Float16, 128); }
     } else if (dtype == DT_F32) {
-        if (a.D == 64) { OFH_DISPATCH_GM(flash_fwd_mfma32_kernel, 64); }
-        if (a.D == 128) { OFH_DISPATCH_GM(flash_fwd_mfma32_kernel, 128); }
+        if (a.D == 64) { OFH_DISPATCH_GM(flash_fwd_mfma32_kernel, kThreads32, 64); }
+        if (a.D == 128) { OFH_DISPATCH_GM(flash_fwd_mfma32_kernel, kThreads32, 128); }
     }
 #undef OFH_DISPATCH_GM
     return hipErrorInvalidValue;
@@ -600,6 +713,9 @@ const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod) {
     return names[dtype][D == 128][general_mod ? 1 : 0];
 }
 
-int flash_mfma_block_n(int dtype) { return dtype == DT_F32 ? kBlockNF32 : kBlockN; }
+MfmaTiles flash_mfma_tiles(int dtype) {
+    if (dtype == DT_F32) return MfmaTiles{kBlockM32, kBlockNF32, kThreads32};
+    return MfmaTiles{kBlockM16, kBlockN16, kThreads16};
+}
 
 }  // namespace ofh

@@ -10,13 +10,15 @@ namespace ofh {
 enum DType : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
 enum Bias : int { BIAS_NONE = 0, BIAS_ALIBI = 1, BIAS_DENSE = 2 };
 
-// Tile shape of the MFMA flash kernels: 4 wavefronts, each owning 32 query
-// rows (one 32-wide MFMA column block), K/V streamed in tiles of 64 keys.
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
+// Every wavefront of the MFMA flash kernels owns 32 query rows (one 32-wide
+// MFMA column block); the workgroup shape depends on the element type.
 constexpr int kQueriesPerWave = 32;
-constexpr int kBlockM = kWaves * kQueriesPerWave;  // 128
-constexpr int kBlockN = 64;
+
+struct MfmaTiles {
+    int block_m;  // query rows per workgroup
+    int block_n;  // keys per K/V tile
+    int threads;  // threads per workgroup
+};
 
 // Everything a forward kernel needs, passed by value. Pointers are device
 // pointers; strides are in elements; the last axis of every tensor is
@@ -66,7 +68,7 @@ hipError_t launch_rowwise(const FwdArgs& a, int dtype, hipStream_t s);
 hipError_t launch_tile_lists(const TileListArgs& a, hipStream_t s);
 
 const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod);
-// Keys per K/V tile of the MFMA kernel for a dtype (64 for bf16/fp16, 32 for fp32).
-int flash_mfma_block_n(int dtype);
+// Workgroup tiling of the MFMA kernel for a dtype.
+MfmaTiles flash_mfma_tiles(int dtype);
 
 }  // namespace ofh
