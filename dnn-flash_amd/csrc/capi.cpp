@@ -156,7 +156,8 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
         return OFH_SUCCESS;
     }
     r.algorithm = OFH_ALGO_FLASH_MFMA;
-    const ofh::MfmaTiles tiles = ofh::flash_mfma_tiles(p->dtype);
+    const ofh::MfmaTiles tiles =
+        ofh::flash_mfma_tiles(p->dtype, r.general_mod, p->mask_allowed != nullptr);
     r.block_m = tiles.block_m;
     r.block_n = tiles.block_n;
     r.threads = tiles.threads;
@@ -442,7 +443,7 @@ int ofh_attention_launch_info(const ofh_attention_params* p, ofh_launch_info* in
         info->block_n = r.block_n;
         info->threads = r.threads;
         info->workgroups = (int64_t)p->batch * p->heads * r.num_q_tiles;
-        name = ofh::flash_mfma_kernel_name(p->dtype, (int)p->head_dim, r.general_mod);
+        name = ofh::flash_mfma_kernel_name(p->dtype, (int)p->head_dim, r.general_mod, r.tile_list);
     } else {
         info->block_m = 1;
         info->block_n = 64;

@@ -172,20 +172,26 @@ __device__ __forceinline__ float online_softmax_tile(const FwdArgs& a, f32x16 (&
 // ---------------------------------------------------------------------------
 // bf16 / fp16 inputs, fp32 accumulate: v_mfma_f32_32x32x16_{bf16,f16}.
 //
-// 8 wavefronts x 32 query rows = 256 queries per workgroup, 2 wavefronts per
-// SIMD so that one wavefront's softmax (VALU) overlaps the other's MFMAs.
-// K/V tiles of 64 keys are staged global -> registers -> LDS one tile ahead,
-// double-buffered, one barrier per tile. Loads are unconditional (rows past
-// the end are clamped to the last row, their V values zeroed, their scores
-// masked), so no exec-masked branches break the compiler's wait counting.
+// Every wavefront owns 32 query rows. K/V tiles of 64 keys are staged
+// global -> registers -> LDS one tile ahead. Loads are unconditional: rows
+// past the end are clamped to the last row, their V zeroed and their scores
+// masked, so no exec-masked branch breaks the compiler's wait counting.
 //
-// LDS layout: both tiles row-major [key][d] with the 16-byte chunk index of
-// each row XOR-swizzled. The K swizzle makes the A-operand reads (16 rows
-// kappa(0..15) at one chunk column per 16 lanes) hit 16 distinct bank quads;
-// the V swizzle makes the ds_read_b64_tr_b16 reads (rows {0..3} x 4 chunk
-// columns per instruction half) hit distinct bank quads. The transposed read
-// delivers V^T fragments directly, so V is never transposed in a separate
-// pass.
+// LDS layout: both tiles row-major [key][d] with padded row strides chosen
+// so that the K A-operand reads (ds_read_b128) and the V reads
+// (ds_read_b64_tr_b16, which deliver V^T fragments directly, so V is never
+// transposed in a separate pass) are free of bank conflicts, with every
+// per-read offset a compile-time immediate.
+//
+// Two workgroup schedules share this tile code:
+//  * ping-pong (plain scale, no block mask): 8 wavefronts in two groups of 4.
+//    While group 0 runs its matrix phase (O += P_{i-1} V_{i-1}; S_i = K_i Q^T)
+//    group 1 runs its softmax phase on the same SIMDs, and the roles swap at
+//    every barrier. Three LDS stages.
+//  * lockstep (score_mod, block-mask lists): all wavefronts run S, softmax
+//    and PV of a tile between two barriers; double-buffered LDS. With a
+//    block-mask list the workgroup has 4 wavefronts (128 query rows), which
+//    wastes fewer partial tiles on fine masks.
 //
 // Online softmax with lazy rescaling: the running max m that probabilities
 // are taken against is raised only when a tile's max exceeds it by more than
@@ -193,9 +199,6 @@ __device__ __forceinline__ float online_softmax_tile(const FwdArgs& a, f32x16 (&
 // branch) runs on a few tiles per row instead of every tile. The result is
 // exact in real arithmetic: O and l share the same stale max.
 
-constexpr int kWaves16 = 8;
-constexpr int kThreads16 = kWaves16 * 64;
-constexpr int kBlockM16 = kWaves16 * kQueriesPerWave;  // 256
 constexpr int kBlockN16 = 64;
 constexpr float kRescaleSlack = 8.0f;
 
@@ -203,18 +206,23 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef short i16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 
 template <int D>
 struct TileLayout {
-    static constexpr int RB = D * 2;             // bytes per K/V row
-    static constexpr int CPR = D / 8;            // 16-byte chunks per row
-    static constexpr int TILE = kBlockN16 * RB;  // bytes of one K (or V) tile
-    static __device__ __forceinline__ int kswz(int row) { return D == 128 ? (row & 15) : ((row >> 1) & 7); }
-    static __device__ __forceinline__ int vswz(int row) {
-        return D == 128 ? ((row & 3) << 2) : (((row >> 1) & 1) << 2);
-    }
-    static __device__ __forceinline__ int kaddr(int row, int chunk) { return row * RB + ((chunk ^ kswz(row)) << 4); }
-    static __device__ __forceinline__ int vaddr(int row, int chunk) { return row * RB + ((chunk ^ vswz(row)) << 4); }
+    static constexpr int RB = D * 2;              // bytes of one K/V row
+    static constexpr int CPR = D / 8;             // 16-byte chunks per row
+    // Row strides with padding. K: rows kappa(0..15) read at one chunk column
+    // by 16 lanes land in 16 distinct 16-byte bank groups (stride/16 odd).
+    // V: the transposed reads of rows {k..k+3} x 4 chunk columns land in 4
+    // distinct groups of 4 (stride/16 = 4 mod 8 for D=128, 12 for D=64).
+    static constexpr int KSTR = RB + 16;
+    static constexpr int VSTR = RB + 64;
+    static constexpr int KTILE = kBlockN16 * KSTR;
+    static constexpr int VTILE = kBlockN16 * VSTR;
+    static constexpr int STAGE = KTILE + VTILE;   // K tile then V tile
+    static __device__ __forceinline__ int kaddr(int row, int chunk) { return row * KSTR + (chunk << 4); }
+    static __device__ __forceinline__ int vaddr(int row, int chunk) { return row * VSTR + (chunk << 4); }
 };
 
 // max over both 32-lane halves (lane l and l^32 hold the same query row)
@@ -241,234 +249,241 @@ struct Dot2<_Float16> {
     }
 };
 
-template <typename T, int D, bool GENERAL>
-__global__ __launch_bounds__(kThreads16) void flash_fwd_mfma16_kernel(FwdArgs a) {
+// The per-wavefront state and the tile operations of one 32-row wavefront.
+template <typename T, int D, bool GENERAL, int NTHREADS>
+struct Wave32 {
     using M16 = Mfma16<T>;
     using v8 = typename M16::v8;
     using L = TileLayout<D>;
-    constexpr int BN = kBlockN16;
-    constexpr int CPT = BN * L::CPR / kThreads16;  // 16-byte chunks per thread per tile
-    static_assert(CPT >= 1 && BN * L::CPR % kThreads16 == 0, "tile must split evenly");
+    static constexpr int BN = kBlockN16;
+    static constexpr int CPT = BN * L::CPR / NTHREADS;  // 16-byte chunks per thread per tile
+    static_assert(CPT >= 1 && BN * L::CPR % NTHREADS == 0, "tile must split evenly");
 
-    __shared__ __attribute__((aligned(16))) unsigned char smem[4 * L::TILE];  // K0 V0 K1 V1
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int g = lane >> 5, r = lane & 31;
-
-    int bh, qt;
-    map_work(blockIdx.x, a.B * a.H, a.num_q_tiles, a.causal, bh, qt);
-    const int b = bh / a.H, h = bh - b * a.H;
-    const T* __restrict__ Qp = (const T*)a.q + b * a.q_sb + h * a.q_sh;
-    const T* __restrict__ Kp = (const T*)a.k + b * a.k_sb + h * a.k_sh;
-    const T* __restrict__ Vp = (const T*)a.v + b * a.v_sb + h * a.v_sh;
-    const int q0 = qt * kBlockM16;
-    const int qw0 = q0 + wave * kQueriesPerWave;
-    const int my_q = qw0 + r;
-
-    // Q^T fragments (B operand of S^T = K Q^T): lane holds Q[my_q][16c + 8g .. +7].
+    const FwdArgs& a;
+    unsigned char* smem;
+    const T* Kp;
+    const T* Vp;
+    int tid, g, h, b;
+    int qw0, my_q;
+    int ntiles;
+    const int* list;
     v8 qf[D / 16];
-    {
+    f32x16 o[D / 32];
+    f32x16 s[BN / 32];
+    v8 pf[BN / 16];
+    float m_run, l_run;
+    float slope;
+    const float* bias_row;
+    // staging
+    int ld_row[CPT], ld_koff[CPT], ld_voff[CPT], st_koff[CPT], st_voff[CPT];
+    u32x4 kreg[CPT], vreg[CPT];
+    int staged_kt;
+    // LDS read lane offsets
+    int k_lane_off, v_lane_off;
+
+    __device__ __forceinline__ Wave32(const FwdArgs& args, unsigned char* sm, int bh, int q0, int wave)
+        : a(args), smem(sm) {
+        tid = threadIdx.x;
+        const int lane = tid & 63;
+        g = lane >> 5;
+        const int r = lane & 31;
+        b = bh / a.H;
+        h = bh - b * a.H;
+        const T* Qp = (const T*)a.q + b * a.q_sb + h * a.q_sh;
+        Kp = (const T*)a.k + b * a.k_sb + h * a.k_sh;
+        Vp = (const T*)a.v + b * a.v_sb + h * a.v_sh;
+        qw0 = q0 + wave * kQueriesPerWave;
+        my_q = qw0 + r;
+        // Q^T fragments (B operand of S^T = K Q^T): lane holds Q[my_q][16c + 8g .. +7].
         const T* qrow = Qp + (int64_t)min(my_q, a.M - 1) * a.q_sm + 8 * g;
 #pragma unroll
         for (int c = 0; c < D / 16; ++c) qf[c] = __builtin_bit_cast(v8, *(const u32x4*)(qrow + 16 * c));
-    }
-
-    int ntiles;
-    const int* list = nullptr;
-    if (a.tile_counts != nullptr) {
-        ntiles = a.tile_counts[qt];
-        list = a.tile_entries + (int64_t)qt * a.num_k_tiles;
-    } else {
-        const int kend = a.causal ? min(a.N, q0 + kBlockM16) : a.N;
-        ntiles = (kend + BN - 1) / BN;
-    }
-    auto tile_at = [&](int it, bool& partial) -> int {
-        if (list != nullptr) {
-            const int e = list[it];
-            partial = (e & 1) != 0;
-            return e >> 1;
-        }
-        partial = false;
-        return it;
-    };
-
-    // Global -> register staging of one K/V tile; rows past N are clamped to N-1.
-    u32x4 kreg[CPT], vreg[CPT];
-    auto load_tile = [&](int kt) {
-        const int k0 = kt * BN;
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) o[db] = f32x16{};
+        m_run = kNegInf;
+        l_run = 0.0f;
+        slope = (GENERAL && a.bias_kind == BIAS_ALIBI) ? a.alibi[h] : 0.0f;
+        bias_row = nullptr;
+        if (GENERAL && a.bias_kind == BIAS_DENSE && my_q < a.M)
+            bias_row = a.bias + b * a.bias_sb + h * a.bias_sh + (int64_t)my_q * a.bias_sm;
 #pragma unroll
         for (int u = 0; u < CPT; ++u) {
-            const int ci = tid + kThreads16 * u;
-            const int row = ci / L::CPR, c = ci % L::CPR;
-            const int kj = min(k0 + row, a.N - 1);
-            kreg[u] = *(const u32x4*)(Kp + (int64_t)kj * a.k_sn + 8 * c);
-            vreg[u] = *(const u32x4*)(Vp + (int64_t)kj * a.v_sn + 8 * c);
+            const int ci = tid + NTHREADS * u;
+            ld_row[u] = ci / L::CPR;
+            ld_koff[u] = ld_row[u] * (int)a.k_sn + 8 * (ci % L::CPR);
+            ld_voff[u] = ld_row[u] * (int)a.v_sn + 8 * (ci % L::CPR);
+            st_koff[u] = L::kaddr(ci / L::CPR, ci % L::CPR);
+            st_voff[u] = L::KTILE + L::vaddr(ci / L::CPR, ci % L::CPR);
         }
-    };
-    auto store_tile = [&](int buf, int kt) {
-        unsigned char* Kb = smem + buf * 2 * L::TILE;
-        unsigned char* Vb = Kb + L::TILE;
+        staged_kt = 0;
+        // K: A-operand row kappa(r) of a 32-key block, chunk 2c+g. V (transposed
+        // reads): input lane j of a 16-lane group reads key (j/4) of a 4-key
+        // group at d-chunk cmap(j%4) of the group's 16 columns; cmap = {0,2,1,3}
+        // applies kappa to the output rows.
+        const int G = lane >> 4, j = lane & 15;
+        k_lane_off = kappa(r) * L::KSTR + 16 * g;
+        const int v_dquad = 16 * (G & 1) + 4 * ((j & 1) * 2 + ((j >> 1) & 1));  // d offset within 32
+        v_lane_off = L::KTILE + (8 * g + (j >> 2)) * L::VSTR + (v_dquad >> 3) * 16 + (v_dquad & 4) * 2;
+    }
+
+    __device__ __forceinline__ int tile_of(int it) const { return list != nullptr ? (list[it] >> 1) : it; }
+    __device__ __forceinline__ bool tile_partial(int it) const { return list != nullptr && (list[it] & 1) != 0; }
+    __device__ __forceinline__ bool tile_active(int kt) const {
+        return qw0 < a.M && !(a.causal && kt * BN > qw0 + kQueriesPerWave - 1);
+    }
+    __device__ __forceinline__ bool tile_needs_mask(int it, int kt) const {
+        return list != nullptr ? tile_partial(it)
+                               : ((kt * BN + BN > a.N) || (a.causal && kt * BN + BN - 1 > qw0));
+    }
+
+    // Global -> register staging of this thread's share of one K/V tile: a
+    // uniform tile base plus fixed 32-bit lane offsets; in the last, ragged
+    // tile rows past N are clamped to N-1.
+    __device__ __forceinline__ void load_tile(int kt) {
         const int k0 = kt * BN;
+        staged_kt = kt;
+        const T* kt_base = Kp + (int64_t)k0 * a.k_sn;
+        const T* vt_base = Vp + (int64_t)k0 * a.v_sn;
+        if (k0 + BN <= a.N) {
+#pragma unroll
+            for (int u = 0; u < CPT; ++u) {
+                kreg[u] = *(const u32x4*)(kt_base + ld_koff[u]);
+                vreg[u] = *(const u32x4*)(vt_base + ld_voff[u]);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < CPT; ++u) {
+                const int back = max(0, k0 + ld_row[u] - (a.N - 1));  // rows to step back
+                kreg[u] = *(const u32x4*)(kt_base + ld_koff[u] - back * (int)a.k_sn);
+                vreg[u] = *(const u32x4*)(vt_base + ld_voff[u] - back * (int)a.v_sn);
+            }
+        }
+    }
+    __device__ __forceinline__ void store_tile(int stage_off) {
+        unsigned char* base = smem + stage_off;
+        const int k0 = staged_kt * BN;
 #pragma unroll
         for (int u = 0; u < CPT; ++u) {
-            const int ci = tid + kThreads16 * u;
-            const int row = ci / L::CPR, c = ci % L::CPR;
-            *(u32x4*)(Kb + L::kaddr(row, c)) = kreg[u];
+            *(u32x4*)(base + st_koff[u]) = kreg[u];
             const u32x4 zero = {0u, 0u, 0u, 0u};
-            *(u32x4*)(Vb + L::vaddr(row, c)) = (k0 + row < a.N) ? vreg[u] : zero;
+            *(u32x4*)(base + st_voff[u]) = (k0 + ld_row[u] < a.N) ? vreg[u] : zero;
         }
-    };
-
-    // Per-lane constants of the transposed V reads: input lane j of a 16-lane
-    // group reads key (j/4) of a 4-key group at d-chunk cmap(j%4) of the lane
-    // group's 16 columns; cmap = {0,2,1,3} applies kappa to the output rows.
-    const int G = lane >> 4, j = lane & 15;
-    const int v_key = 8 * g + (j >> 2);
-    const int v_dquad = 16 * (G & 1) + 4 * ((j & 1) * 2 + ((j >> 1) & 1));  // d offset within 32
-    // K A-operand row of this lane within a 32-key block
-    const int k_row = kappa(r);
-
-    f32x16 o[D / 32];
-#pragma unroll
-    for (int db = 0; db < D / 32; ++db) o[db] = f32x16{};
-    float m_run = kNegInf, l_run = 0.0f;
-    const float slope = (GENERAL && a.bias_kind == BIAS_ALIBI) ? a.alibi[h] : 0.0f;
-    const float* bias_row = nullptr;
-    if (GENERAL && a.bias_kind == BIAS_DENSE && my_q < a.M)
-        bias_row = a.bias + b * a.bias_sb + h * a.bias_sh + (int64_t)my_q * a.bias_sm;
-    const bool wave_has_rows = qw0 < a.M;
-
-    if (ntiles > 0) {
-        bool p0;
-        const int kt0 = tile_at(0, p0);
-        load_tile(kt0);
-        store_tile(0, kt0);
     }
-    __syncthreads();
 
-    for (int it = 0; it < ntiles; ++it) {
-        bool partial;
-        const int kt = tile_at(it, partial);
-        int kt_next = 0;
-        if (it + 1 < ntiles) {
-            bool pn;
-            kt_next = tile_at(it + 1, pn);
-            load_tile(kt_next);
+    // S^T = K Q^T for the tile in LDS stage `stage_off`
+    __device__ __forceinline__ void qk(int stage_off) {
+        const lds_u8* kb = (const lds_u8*)smem + stage_off + k_lane_off;
+#pragma unroll
+        for (int sb = 0; sb < BN / 32; ++sb) {
+            s[sb] = f32x16{};
+#pragma unroll
+            for (int c = 0; c < D / 16; ++c) {
+                const v8 af = __builtin_bit_cast(v8, *(const lds_u32x4*)(kb + 32 * sb * L::KSTR + 32 * c));
+                s[sb] = M16::mma(af, qf[c], s[sb]);
+            }
         }
-        const unsigned char* Kb = smem + (it & 1) * 2 * L::TILE;
-        const unsigned char* Vb = Kb + L::TILE;
+    }
+
+    // O^T += V^T P^T for the tile in LDS stage `stage_off` (A operand from two
+    // transposed 4-key reads)
+    __device__ __forceinline__ void pv(int stage_off) {
+        const lds_u8* vb = (const lds_u8*)smem + stage_off + v_lane_off;
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) {
+#pragma unroll
+            for (int c = 0; c < BN / 16; ++c) {
+                const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_i16x4*)(vb + (16 * c) * L::VSTR + 64 * db));
+                const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_i16x4*)(vb + (16 * c + 4) * L::VSTR + 64 * db));
+                const i16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                o[db] = M16::mma(__builtin_bit_cast(v8, both), pf[c], o[db]);
+            }
+        }
+    }
+
+    // Online softmax of the scores in s (tile of iteration `it`): running
+    // max with lazy rescale of O and l, probabilities packed into pf, row sum.
+    __device__ __forceinline__ void softmax(int it) {
+        const int kt = tile_of(it);
         const int k0 = kt * BN;
-        const bool active = wave_has_rows && !(a.causal && k0 > qw0 + kQueriesPerWave - 1);
-        if (active) {
-            const bool need_mask = list != nullptr
-                                       ? partial
-                                       : ((k0 + BN > a.N) || (a.causal && k0 + BN - 1 > qw0));
-            // S^T = K Q^T for 64 keys: two 32x32 blocks.
-            f32x16 s[BN / 32];
+        const bool need_mask = tile_needs_mask(it, kt);
+        float mx = kNegInf;
+        if (!GENERAL && !need_mask) {
+            if (a.scale_log2 >= 0.0f) {
 #pragma unroll
-            for (int sb = 0; sb < BN / 32; ++sb) {
-                s[sb] = f32x16{};
-                const int row = 32 * sb + k_row;
+                for (int sb = 0; sb < BN / 32; ++sb)
 #pragma unroll
-                for (int c = 0; c < D / 16; ++c) {
-                    const v8 af = __builtin_bit_cast(v8, *(const u32x4*)(Kb + L::kaddr(row, 2 * c + g)));
-                    s[sb] = M16::mma(af, qf[c], s[sb]);
+                    for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[sb][e]);
+                mx *= a.scale_log2;
+            } else {
+                float mn = __builtin_huge_valf();
+#pragma unroll
+                for (int sb = 0; sb < BN / 32; ++sb)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) mn = fminf(mn, s[sb][e]);
+                mx = mn * a.scale_log2;
+            }
+        } else {
+            const bool row_out = GENERAL && my_q >= a.M;
+#pragma unroll
+            for (int sb = 0; sb < BN / 32; ++sb)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int kj = k0 + 32 * sb + acc_pos(e, g);
+                    const bool msk = row_out || (need_mask && elem_masked(a, my_q, kj));
+                    float x = kNegInf;
+                    if (!msk) {
+                        x = GENERAL ? general_score(a, s[sb][e], my_q, kj, slope, bias_row)
+                                    : s[sb][e] * a.scale_log2;
+                    }
+                    s[sb][e] = x;
+                    mx = fmaxf(mx, x);
                 }
-            }
+        }
+        mx = half_swap_max(mx);
 
-            // Scores in log2 units; masked entries -inf.
-            float mx = kNegInf;
-            if (!GENERAL && !need_mask) {
-                float smax = kNegInf, smin = __builtin_huge_valf();
+        // Lazy rescale (wave-uniform branch).
+        const bool raise = mx > m_run + kRescaleSlack;
+        if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+            // lanes that do not raise keep their max and scale by exactly 1
+            // (their m_run may be -inf: -inf - -inf must not reach exp2)
+            const float alpha = raise ? __builtin_amdgcn_exp2f(m_run - mx) : 1.0f;
+            m_run = raise ? mx : m_run;
+            l_run *= alpha;
 #pragma unroll
-                for (int sb = 0; sb < BN / 32; ++sb)
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        smax = fmaxf(smax, s[sb][e]);
-                        smin = fminf(smin, s[sb][e]);
-                    }
-                mx = a.scale_log2 >= 0.0f ? smax * a.scale_log2 : smin * a.scale_log2;
-            } else {
-                const bool row_out = GENERAL && my_q >= a.M;
-#pragma unroll
-                for (int sb = 0; sb < BN / 32; ++sb)
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        const int kj = k0 + 32 * sb + acc_pos(e, g);
-                        const bool msk = row_out || (need_mask && elem_masked(a, my_q, kj));
-                        float x = kNegInf;
-                        if (!msk) {
-                            x = GENERAL ? general_score(a, s[sb][e], my_q, kj, slope, bias_row)
-                                        : s[sb][e] * a.scale_log2;
-                        }
-                        s[sb][e] = x;
-                        mx = fmaxf(mx, x);
-                    }
-            }
-            mx = half_swap_max(mx);
+            for (int db = 0; db < D / 32; ++db) o[db] *= alpha;
+        }
+        const float m_use = (m_run == kNegInf) ? 0.0f : m_run;
 
-            // Lazy rescale (wave-uniform branch).
-            const bool raise = mx > m_run + kRescaleSlack;
-            if (__builtin_amdgcn_ballot_w64(raise) != 0) {
-                // lanes that do not raise keep their max and scale by exactly 1
-                // (their m_run may be -inf: -inf - -inf must not reach exp2)
-                const float alpha = raise ? __builtin_amdgcn_exp2f(m_run - mx) : 1.0f;
-                m_run = raise ? mx : m_run;
-                l_run *= alpha;
-#pragma unroll
-                for (int db = 0; db < D / 32; ++db) o[db] *= alpha;
-            }
-            const float m_use = (m_run == kNegInf) ? 0.0f : m_run;
-
-            // Probabilities, packed to the MFMA input type; row sum from the packed values.
-            v8 pf[BN / 16];
-            if (!GENERAL && !need_mask) {
-#pragma unroll
-                for (int c = 0; c < BN / 16; ++c)
-#pragma unroll
-                    for (int t = 0; t < 8; ++t)
-                        pf[c][t] = (T)__builtin_amdgcn_exp2f(
-                            __builtin_fmaf(s[c >> 1][8 * (c & 1) + t], a.scale_log2, -m_use));
-            } else {
-#pragma unroll
-                for (int c = 0; c < BN / 16; ++c)
-#pragma unroll
-                    for (int t = 0; t < 8; ++t)
-                        pf[c][t] = (T)__builtin_amdgcn_exp2f(s[c >> 1][8 * (c & 1) + t] - m_use);
-            }
-            float lsum = 0.0f;
+        if (!GENERAL && !need_mask) {
 #pragma unroll
             for (int c = 0; c < BN / 16; ++c)
 #pragma unroll
-                for (int t = 0; t < 8; t += 2)
-                    lsum = Dot2<T>::sum2(typename Dot2<T>::v2{pf[c][t], pf[c][t + 1]}, lsum);
-            l_run += lsum;
-
-            // O^T += V^T P^T: A operand from two transposed 4-key reads.
+                for (int t = 0; t < 8; ++t)
+                    pf[c][t] = (T)__builtin_amdgcn_exp2f(
+                        __builtin_fmaf(s[c >> 1][8 * (c & 1) + t], a.scale_log2, -m_use));
+        } else {
 #pragma unroll
-            for (int db = 0; db < D / 32; ++db) {
-                const int d = 32 * db + v_dquad;
-                const int chunk = d >> 3, half = (d & 4) * 2;  // byte offset 0 or 8 in the chunk
+            for (int c = 0; c < BN / 16; ++c)
 #pragma unroll
-                for (int c = 0; c < BN / 16; ++c) {
-                    const int key = 16 * c + v_key;
-                    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (lds_i16x4*)((lds_u8*)Vb + L::vaddr(key, chunk) + half));
-                    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (lds_i16x4*)((lds_u8*)Vb + L::vaddr(key + 4, chunk) + half));
-                    const i16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                    o[db] = M16::mma(__builtin_bit_cast(v8, both), pf[c], o[db]);
-                }
-            }
+                for (int t = 0; t < 8; ++t)
+                    pf[c][t] = (T)__builtin_amdgcn_exp2f(s[c >> 1][8 * (c & 1) + t] - m_use);
         }
-        if (it + 1 < ntiles) store_tile((it + 1) & 1, kt_next);
-        __syncthreads();
+        float lsum = 0.0f;
+#pragma unroll
+        for (int c = 0; c < BN / 16; ++c)
+#pragma unroll
+            for (int t = 0; t < 8; t += 2)
+                lsum = Dot2<T>::sum2(typename Dot2<T>::v2{pf[c][t], pf[c][t + 1]}, lsum);
+        l_run += lsum;
     }
 
-    // Normalise; rows that saw no valid key have l = 0 and are written as 0.
-    const float l_tot = l_run + __shfl_xor(l_run, 32);
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (my_q < a.M) {
+    // Normalise and store; rows that saw no valid key have l = 0 and are written as 0.
+    __device__ __forceinline__ void store_output() {
+        const float l_tot = l_run + __shfl_xor(l_run, 32);
+        const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        if (my_q >= a.M) return;
         if (a.out_f32) {
             float* orow = (float*)a.o + b * a.o_sb + h * a.o_sh + (int64_t)my_q * a.o_sm + 8 * g;
 #pragma unroll
@@ -499,6 +514,109 @@ __global__ __launch_bounds__(kThreads16) void flash_fwd_mfma16_kernel(FwdArgs a)
             }
         }
     }
+};
+
+// Tiles of the workgroup's query block: ntiles and the block-mask list.
+__device__ __forceinline__ void tile_range(const FwdArgs& a, int qt, int block_m, int& ntiles,
+                                           const int*& list) {
+    list = nullptr;
+    if (a.tile_counts != nullptr) {
+        ntiles = a.tile_counts[qt];
+        list = a.tile_entries + (int64_t)qt * a.num_k_tiles;
+    } else {
+        const int q0 = qt * block_m;
+        const int kend = a.causal ? min(a.N, q0 + block_m) : a.N;
+        ntiles = (kend + kBlockN16 - 1) / kBlockN16;
+    }
+}
+
+constexpr int kPingPongThreads = 512;
+constexpr int kPingPongBlockM = 256;
+
+template <typename T, int D>
+__global__ __launch_bounds__(kPingPongThreads) void flash_fwd_pingpong_kernel(FwdArgs a) {
+    using W = Wave32<T, D, false, kPingPongThreads>;
+    using L = typename W::L;
+    constexpr int kStages = 3;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[kStages * L::STAGE];
+    const int wave = threadIdx.x >> 6;
+    const int group = wave >> 2;  // waves w and w+4 share a SIMD
+    int bh, qt;
+    map_work(blockIdx.x, a.B * a.H, a.num_q_tiles, a.causal, bh, qt);
+    W w(a, smem, bh, qt * kPingPongBlockM, wave);
+    tile_range(a, qt, kPingPongBlockM, w.ntiles, w.list);
+    const int ntiles = w.ntiles;
+
+    // stage byte offsets of iterations it-1, it, it+1 (rotated every iteration)
+    int stage_prev = 2 * L::STAGE, stage_cur = 0, stage_next = L::STAGE;
+    // matrix phase of iteration `it`: O += P_{it-1} V_{it-1}; S_it = K_it Q^T
+    auto matrix_phase = [&](int it) {
+        __builtin_amdgcn_s_setprio(1);
+        if (it + 1 < ntiles) w.store_tile(stage_next);
+        if (it + 2 < ntiles) w.load_tile(w.tile_of(it + 2));
+        if (it > 0 && w.tile_active(w.tile_of(it - 1))) w.pv(stage_prev);
+        if (it < ntiles && w.tile_active(w.tile_of(it))) w.qk(stage_cur);
+        const int t = stage_prev;
+        stage_prev = stage_cur;
+        stage_cur = stage_next;
+        stage_next = t;
+    };
+    auto softmax_phase = [&](int it) {
+        __builtin_amdgcn_s_setprio(0);
+        if (w.tile_active(w.tile_of(it))) w.softmax(it);
+    };
+
+    if (ntiles > 0) {
+        w.load_tile(w.tile_of(0));
+        w.store_tile(0);
+        if (ntiles > 1) w.load_tile(w.tile_of(1));
+    }
+    __syncthreads();
+    if (group == 1) __syncthreads();  // group 1 runs one phase behind
+    for (int it = 0; it < ntiles; ++it) {
+        matrix_phase(it);
+        __syncthreads();
+        softmax_phase(it);
+        __syncthreads();
+    }
+    if (ntiles > 0) matrix_phase(ntiles);  // last O += P V
+    __syncthreads();
+    if (group == 0) __syncthreads();  // same barrier count for both groups
+    __builtin_amdgcn_s_setprio(0);
+    w.store_output();
+}
+
+template <typename T, int D, bool GENERAL, int NWAVES>
+__global__ __launch_bounds__(NWAVES * 64, 8 / NWAVES) void flash_fwd_lockstep_kernel(FwdArgs a) {
+    constexpr int NTHREADS = NWAVES * 64;
+    constexpr int BLOCK_M = NWAVES * kQueriesPerWave;
+    using W = Wave32<T, D, GENERAL, NTHREADS>;
+    using L = typename W::L;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[2 * L::STAGE];
+    const int wave = threadIdx.x >> 6;
+    int bh, qt;
+    map_work(blockIdx.x, a.B * a.H, a.num_q_tiles, a.causal, bh, qt);
+    W w(a, smem, bh, qt * BLOCK_M, wave);
+    tile_range(a, qt, BLOCK_M, w.ntiles, w.list);
+    const int ntiles = w.ntiles;
+
+    if (ntiles > 0) {
+        w.load_tile(w.tile_of(0));
+        w.store_tile(0);
+    }
+    __syncthreads();
+    for (int it = 0; it < ntiles; ++it) {
+        if (it + 1 < ntiles) w.load_tile(w.tile_of(it + 1));
+        const int stage = (it & 1) * L::STAGE;
+        if (w.tile_active(w.tile_of(it))) {
+            w.qk(stage);
+            w.softmax(it);
+            w.pv(stage);
+        }
+        if (it + 1 < ntiles) w.store_tile(((it + 1) & 1) * L::STAGE);
+        __syncthreads();
+    }
+    w.store_output();
 }
 
 // ---------------------------------------------------------------------------
@@ -682,40 +800,68 @@ hipError_t launch(K kernel, int threads, const FwdArgs& a, hipStream_t s) {
 
 }  // namespace
 
-hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipStream_t s) {
-#define OFH_DISPATCH_GM(KERNEL, THREADS, ...)                                   \
-    return general_mod ? launch(KERNEL<__VA_ARGS__, true>, THREADS, a, s)        \
-                       : launch(KERNEL<__VA_ARGS__, false>, THREADS, a, s)
-    if (dtype == DT_BF16) {
-        if (a.D == 64) { OFH_DISPATCH_GM(flash_fwd_mfma16_kernel, kThreads16, __bf16, 64); }
-        if (a.D == 128) { OFH_DISPATCH_GM(flash_fwd_mfma16_kernel, kThreads16, __bf16, 128); }
-    } else if (dtype == DT_F16) {
-        if (a.D == 64) { OFH_DISPATCH_GM(flash_fwd_mfma16_kernel, kThreads16, _Float16, 64); }
-        if (a.D == 128) { OFH_DISPATCH_GM(flash_fwd_mfma16_kernel, kThreads16, _Float16, 128); }
-    } else if (dtype == DT_F32) {
-        if (a.D == 64) { OFH_DISPATCH_GM(flash_fwd_mfma32_kernel, kThreads32, 64); }
-        if (a.D == 128) { OFH_DISPATCH_GM(flash_fwd_mfma32_kernel, kThreads32, 128); }
+// 16-bit kernel schedule for a call: ping-pong for the plain scale without a
+// block-mask list, lockstep otherwise (4 wavefronts with a list, 8 without).
+enum Sched16 { SCHED_PINGPONG = 0, SCHED_LOCKSTEP8 = 1, SCHED_LOCKSTEP4 = 2 };
+
+static int sched16(bool general_mod, bool tile_list) {
+    if (tile_list) return SCHED_LOCKSTEP4;
+    return general_mod ? SCHED_LOCKSTEP8 : SCHED_PINGPONG;
+}
+
+template <typename T, int D>
+static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
+    switch (sched16(general_mod, a.tile_counts != nullptr)) {
+        case SCHED_PINGPONG:
+            return launch(flash_fwd_pingpong_kernel<T, D>, kPingPongThreads, a, s);
+        case SCHED_LOCKSTEP8:
+            return general_mod ? launch(flash_fwd_lockstep_kernel<T, D, true, 8>, 512, a, s)
+                               : launch(flash_fwd_lockstep_kernel<T, D, false, 8>, 512, a, s);
+        default:
+            return general_mod ? launch(flash_fwd_lockstep_kernel<T, D, true, 4>, 256, a, s)
+                               : launch(flash_fwd_lockstep_kernel<T, D, false, 4>, 256, a, s);
     }
-#undef OFH_DISPATCH_GM
+}
+
+hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipStream_t s) {
+    if (dtype == DT_BF16) {
+        if (a.D == 64) return launch16<__bf16, 64>(a, general_mod, s);
+        if (a.D == 128) return launch16<__bf16, 128>(a, general_mod, s);
+    } else if (dtype == DT_F16) {
+        if (a.D == 64) return launch16<_Float16, 64>(a, general_mod, s);
+        if (a.D == 128) return launch16<_Float16, 128>(a, general_mod, s);
+    } else if (dtype == DT_F32) {
+        if (a.D == 64)
+            return general_mod ? launch(flash_fwd_mfma32_kernel<64, true>, kThreads32, a, s)
+                               : launch(flash_fwd_mfma32_kernel<64, false>, kThreads32, a, s);
+        if (a.D == 128)
+            return general_mod ? launch(flash_fwd_mfma32_kernel<128, true>, kThreads32, a, s)
+                               : launch(flash_fwd_mfma32_kernel<128, false>, kThreads32, a, s);
+    }
     return hipErrorInvalidValue;
 }
 
-const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod) {
-    static const char* names[3][2][2] = {
-        {{"flash_fwd_mfma32_kernel<64,plain>", "flash_fwd_mfma32_kernel<64,general>"},
-         {"flash_fwd_mfma32_kernel<128,plain>", "flash_fwd_mfma32_kernel<128,general>"}},
-        {{"flash_fwd_mfma16_kernel<bf16,64,plain>", "flash_fwd_mfma16_kernel<bf16,64,general>"},
-         {"flash_fwd_mfma16_kernel<bf16,128,plain>", "flash_fwd_mfma16_kernel<bf16,128,general>"}},
-        {{"flash_fwd_mfma16_kernel<f16,64,plain>", "flash_fwd_mfma16_kernel<f16,64,general>"},
-         {"flash_fwd_mfma16_kernel<f16,128,plain>", "flash_fwd_mfma16_kernel<f16,128,general>"}},
-    };
+const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile_list) {
     if (dtype < 0 || dtype > 2 || (D != 64 && D != 128)) return "none";
-    return names[dtype][D == 128][general_mod ? 1 : 0];
+    static const char* f32names[2][2] = {
+        {"flash_fwd_mfma32_kernel<64,plain>", "flash_fwd_mfma32_kernel<64,general>"},
+        {"flash_fwd_mfma32_kernel<128,plain>", "flash_fwd_mfma32_kernel<128,general>"}};
+    if (dtype == DT_F32) return f32names[D == 128][general_mod ? 1 : 0];
+    static const char* names[2][2][3] = {
+        {{"flash_fwd_pingpong_kernel<bf16,64>", "flash_fwd_lockstep_kernel<bf16,64,8w>", "flash_fwd_lockstep_kernel<bf16,64,4w>"},
+         {"flash_fwd_pingpong_kernel<bf16,128>", "flash_fwd_lockstep_kernel<bf16,128,8w>", "flash_fwd_lockstep_kernel<bf16,128,4w>"}},
+        {{"flash_fwd_pingpong_kernel<f16,64>", "flash_fwd_lockstep_kernel<f16,64,8w>", "flash_fwd_lockstep_kernel<f16,64,4w>"},
+         {"flash_fwd_pingpong_kernel<f16,128>", "flash_fwd_lockstep_kernel<f16,128,8w>", "flash_fwd_lockstep_kernel<f16,128,4w>"}}};
+    return names[dtype == DT_F16][D == 128][sched16(general_mod, tile_list)];
 }
 
-MfmaTiles flash_mfma_tiles(int dtype) {
+MfmaTiles flash_mfma_tiles(int dtype, bool general_mod, bool tile_list) {
     if (dtype == DT_F32) return MfmaTiles{kBlockM32, kBlockNF32, kThreads32};
-    return MfmaTiles{kBlockM16, kBlockN16, kThreads16};
+    switch (sched16(general_mod, tile_list)) {
+        case SCHED_PINGPONG: return MfmaTiles{kPingPongBlockM, kBlockN16, kPingPongThreads};
+        case SCHED_LOCKSTEP8: return MfmaTiles{256, kBlockN16, 512};
+        default: return MfmaTiles{128, kBlockN16, 256};
+    }
 }
 
 }  // namespace ofh

@@ -67,8 +67,8 @@ hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipS
 hipError_t launch_rowwise(const FwdArgs& a, int dtype, hipStream_t s);
 hipError_t launch_tile_lists(const TileListArgs& a, hipStream_t s);
 
-const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod);
+const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile_list);
 // Workgroup tiling of the MFMA kernel for a dtype.
-MfmaTiles flash_mfma_tiles(int dtype);
+MfmaTiles flash_mfma_tiles(int dtype, bool general_mod, bool tile_list);
 
 }  // namespace ofh
