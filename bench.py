@@ -39,7 +39,30 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cpu count)")
     ap.add_argument("--cpu-heads", type=int, default=0, help="heads in the CPU sample; 0: two per thread")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="instead of attention, time a plain device-to-device copy of BYTES "
+                         "(the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
+
+
+def copy_calibration(nbytes: int, steps: int, warmup: int) -> int:
+    import torch
+
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    print(json.dumps({"copy_bytes": src.numel() * 4, "ms_per_copy": ms,
+                      "GB_per_s_read_plus_write": 2 * src.numel() * 4 / ms / 1e6}))
+    return 0
 
 
 def device_inputs(w, torch):
@@ -108,6 +131,9 @@ def main() -> int:
         print(json.dumps({"error": "this build runs on one GPU: the attention kernel shards by heads "
                                    "with no communication (see DESIGN.md); --gpus must be 1"}))
         return 2
+
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration, args.steps, args.warmup)
 
     import torch
 
