@@ -129,7 +129,7 @@ def main() -> int:
     args = parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: the attention kernel shards by heads "
-                                   "with no communication (see DESIGN.md); --gpus must be 1"}))
+                                   "with no communication; --gpus must be 1"}))
         return 2
 
     if args.copy_calibration:

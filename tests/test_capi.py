@@ -136,7 +136,7 @@ def test_useful_flops_match_workloads(ofh):
                       mask_query_blocks=m.shape[0], mask_key_blocks=m.shape[1])
         p = F.make_params(w.batch, w.heads, w.tokens, w.tokens, w.head_dim, causal=w.causal, **kw)
         assert F.useful_flops(p) == w.useful_flops(), w.name
-    # BASELINE table values
+    # published useful-FLOP and pair counts of these workloads
     assert C.get("c3").useful_flops() == 549_890_031_616
     assert C.get("c5").useful_pairs_per_head() == 19_677_184
     assert int(C.get("c5").mask().sum()) == 4930
