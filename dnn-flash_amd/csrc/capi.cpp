@@ -169,6 +169,8 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
         return set_error(OFH_ERROR_UNSUPPORTED, "grid exceeds 2^31 workgroups");
     if (r.tile_list && (int64_t)r.num_q_tiles * r.num_k_tiles > (int64_t)1 << 31)
         return set_error(OFH_ERROR_UNSUPPORTED, "block-mask tile list too large");
+    if (r.tile_list && (r.block_m > ofh::kQueriesPerWave * ofh::kListSlices || r.num_k_tiles > (1 << 22)))
+        return set_error(OFH_ERROR_UNSUPPORTED, "block-mask tile list entry cannot encode this tiling");
     return OFH_SUCCESS;
 }
 

@@ -208,6 +208,17 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 
+// Score modification of a 16-bit kernel instantiation: the plain scale, or
+// any mix of ALiBi / dense bias / soft-cap selected per call.
+enum ScoreMod { MOD_PLAIN = 0, MOD_GENERAL = 1 };
+
+// s_waitcnt vmcnt(0): every vector-memory load issued so far has returned.
+// Issued once before the tile loop, it tells the compiler's wait-count
+// tracking that the Q fragments are resident on every path into the loop;
+// without it the loop waits on them (and so on every load issued after
+// them, i.e. the K/V prefetch) at each use.
+__device__ __forceinline__ void wait_vm_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 template <int D>
 struct TileLayout {
     static constexpr int RB = D * 2;              // bytes of one K/V row
@@ -249,21 +260,29 @@ struct Dot2<_Float16> {
     }
 };
 
+// Position of accumulator register e of sub-block sb within a 64-key tile,
+// relative to the lane half's first key (8g): 32sb + 16(e>>3) + (e&7).
+__device__ __forceinline__ constexpr int tile_pos(int sb, int e) { return 32 * sb + 16 * (e >> 3) + (e & 7); }
+
 // The per-wavefront state and the tile operations of one 32-row wavefront.
-template <typename T, int D, bool GENERAL, int NTHREADS>
+// A "tile step" is identified by its entry: the key tile index, or with a
+// block-mask list (LIST) the list entry (key tile + per-slice bits).
+template <typename T, int D, int MOD, bool LIST, int NTHREADS>
 struct Wave32 {
     using M16 = Mfma16<T>;
     using v8 = typename M16::v8;
     using L = TileLayout<D>;
     static constexpr int BN = kBlockN16;
     static constexpr int CPT = BN * L::CPR / NTHREADS;  // 16-byte chunks per thread per tile
-    static_assert(CPT >= 1 && BN * L::CPR % NTHREADS == 0, "tile must split evenly");
+    static constexpr int RSTEP = NTHREADS / L::CPR;      // rows between a thread's chunks
+    static_assert(CPT >= 1 && BN * L::CPR % NTHREADS == 0 && NTHREADS % L::CPR == 0,
+                  "tile must split evenly");
 
     const FwdArgs& a;
     unsigned char* smem;
     const T* Kp;
     const T* Vp;
-    int tid, g, h, b;
+    int tid, g, h, b, wave;
     int qw0, my_q;
     int ntiles;
     const int* list;
@@ -274,15 +293,15 @@ struct Wave32 {
     float m_run, l_run;
     float slope;
     const float* bias_row;
-    // staging
-    int ld_row[CPT], ld_koff[CPT], ld_voff[CPT], st_koff[CPT], st_voff[CPT];
+    // staging: chunk u of this thread is row ld_row + u*RSTEP, 16-byte column ld_col
+    int ld_row, ld_koff, ld_voff, st_koff;
     u32x4 kreg[CPT], vreg[CPT];
     int staged_kt;
     // LDS read lane offsets
     int k_lane_off, v_lane_off;
 
-    __device__ __forceinline__ Wave32(const FwdArgs& args, unsigned char* sm, int bh, int q0, int wave)
-        : a(args), smem(sm) {
+    __device__ __forceinline__ Wave32(const FwdArgs& args, unsigned char* sm, int bh, int q0, int wv)
+        : a(args), smem(sm), wave(wv) {
         tid = threadIdx.x;
         const int lane = tid & 63;
         g = lane >> 5;
@@ -295,6 +314,7 @@ struct Wave32 {
         qw0 = q0 + wave * kQueriesPerWave;
         my_q = qw0 + r;
         // Q^T fragments (B operand of S^T = K Q^T): lane holds Q[my_q][16c + 8g .. +7].
+        // Rows past the end read the last row; their results are never stored.
         const T* qrow = Qp + (int64_t)min(my_q, a.M - 1) * a.q_sm + 8 * g;
 #pragma unroll
         for (int c = 0; c < D / 16; ++c) qf[c] = __builtin_bit_cast(v8, *(const u32x4*)(qrow + 16 * c));
@@ -302,19 +322,18 @@ struct Wave32 {
         for (int db = 0; db < D / 32; ++db) o[db] = f32x16{};
         m_run = kNegInf;
         l_run = 0.0f;
-        slope = (GENERAL && a.bias_kind == BIAS_ALIBI) ? a.alibi[h] : 0.0f;
+        slope = 0.0f;
         bias_row = nullptr;
-        if (GENERAL && a.bias_kind == BIAS_DENSE && my_q < a.M)
-            bias_row = a.bias + b * a.bias_sb + h * a.bias_sh + (int64_t)my_q * a.bias_sm;
-#pragma unroll
-        for (int u = 0; u < CPT; ++u) {
-            const int ci = tid + NTHREADS * u;
-            ld_row[u] = ci / L::CPR;
-            ld_koff[u] = ld_row[u] * (int)a.k_sn + 8 * (ci % L::CPR);
-            ld_voff[u] = ld_row[u] * (int)a.v_sn + 8 * (ci % L::CPR);
-            st_koff[u] = L::kaddr(ci / L::CPR, ci % L::CPR);
-            st_voff[u] = L::KTILE + L::vaddr(ci / L::CPR, ci % L::CPR);
+        if (MOD == MOD_GENERAL) {
+            if (a.bias_kind == BIAS_ALIBI) slope = a.alibi[h];
+            if (a.bias_kind == BIAS_DENSE)
+                bias_row = a.bias + b * a.bias_sb + h * a.bias_sh + (int64_t)min(my_q, a.M - 1) * a.bias_sm;
         }
+        ld_row = tid / L::CPR;
+        const int ld_col = tid % L::CPR;
+        ld_koff = ld_row * (int)a.k_sn + 8 * ld_col;
+        ld_voff = ld_row * (int)a.v_sn + 8 * ld_col;
+        st_koff = L::kaddr(ld_row, ld_col);
         staged_kt = 0;
         // K: A-operand row kappa(r) of a 32-key block, chunk 2c+g. V (transposed
         // reads): input lane j of a 16-lane group reads key (j/4) of a 4-key
@@ -326,14 +345,16 @@ struct Wave32 {
         v_lane_off = L::KTILE + (8 * g + (j >> 2)) * L::VSTR + (v_dquad >> 3) * 16 + (v_dquad & 4) * 2;
     }
 
-    __device__ __forceinline__ int tile_of(int it) const { return list != nullptr ? (list[it] >> 1) : it; }
-    __device__ __forceinline__ bool tile_partial(int it) const { return list != nullptr && (list[it] & 1) != 0; }
-    __device__ __forceinline__ bool tile_active(int kt) const {
-        return qw0 < a.M && !(a.causal && kt * BN > qw0 + kQueriesPerWave - 1);
+    // Entry of tile step `it` (a global load with a list: issue it early).
+    __device__ __forceinline__ int entry(int it) const { return LIST ? list[it] : it; }
+    __device__ __forceinline__ int tile_of(int e) const { return LIST ? list_tile(e) : e; }
+    __device__ __forceinline__ bool tile_active(int e) const {
+        if (LIST) return list_any(e, wave);
+        return qw0 < a.M && !(a.causal && e * BN > qw0 + kQueriesPerWave - 1);
     }
-    __device__ __forceinline__ bool tile_needs_mask(int it, int kt) const {
-        return list != nullptr ? tile_partial(it)
-                               : ((kt * BN + BN > a.N) || (a.causal && kt * BN + BN - 1 > qw0));
+    // causal diagonal or ragged end inside the tile
+    __device__ __forceinline__ bool tile_crosses(int kt) const {
+        return (kt * BN + BN > a.N) || (a.causal && kt * BN + BN - 1 > qw0);
     }
 
     // Global -> register staging of this thread's share of one K/V tile: a
@@ -347,26 +368,29 @@ struct Wave32 {
         if (k0 + BN <= a.N) {
 #pragma unroll
             for (int u = 0; u < CPT; ++u) {
-                kreg[u] = *(const u32x4*)(kt_base + ld_koff[u]);
-                vreg[u] = *(const u32x4*)(vt_base + ld_voff[u]);
+                kreg[u] = *(const u32x4*)(kt_base + (int64_t)u * RSTEP * a.k_sn + ld_koff);
+                vreg[u] = *(const u32x4*)(vt_base + (int64_t)u * RSTEP * a.v_sn + ld_voff);
             }
         } else {
 #pragma unroll
             for (int u = 0; u < CPT; ++u) {
-                const int back = max(0, k0 + ld_row[u] - (a.N - 1));  // rows to step back
-                kreg[u] = *(const u32x4*)(kt_base + ld_koff[u] - back * (int)a.k_sn);
-                vreg[u] = *(const u32x4*)(vt_base + ld_voff[u] - back * (int)a.v_sn);
+                // rows past N read row N-1 (their V is zeroed in LDS, their scores masked)
+                const int row = min(k0 + ld_row + u * RSTEP, a.N - 1) - k0 - ld_row;
+                kreg[u] = *(const u32x4*)(kt_base + (int64_t)row * a.k_sn + ld_koff);
+                vreg[u] = *(const u32x4*)(vt_base + (int64_t)row * a.v_sn + ld_voff);
             }
         }
     }
     __device__ __forceinline__ void store_tile(int stage_off) {
         unsigned char* base = smem + stage_off;
         const int k0 = staged_kt * BN;
+        // V chunk of the same (row, column): after the K tile, with the V row stride
+        const int st_voff = st_koff + L::KTILE + ld_row * (L::VSTR - L::KSTR);
 #pragma unroll
         for (int u = 0; u < CPT; ++u) {
-            *(u32x4*)(base + st_koff[u]) = kreg[u];
+            *(u32x4*)(base + st_koff + u * RSTEP * L::KSTR) = kreg[u];
             const u32x4 zero = {0u, 0u, 0u, 0u};
-            *(u32x4*)(base + st_voff[u]) = (k0 + ld_row[u] < a.N) ? vreg[u] : zero;
+            *(u32x4*)(base + st_voff + u * RSTEP * L::VSTR) = (k0 + ld_row + u * RSTEP < a.N) ? vreg[u] : zero;
         }
     }
 
@@ -402,14 +426,111 @@ struct Wave32 {
         }
     }
 
-    // Online softmax of the scores in s (tile of iteration `it`): running
+    // Scores in log2 units with the call's score_mod: scale, then ALiBi
+    // slope*(key - query) or a dense bias, then cap*tanh(x/cap). Constants are
+    // folded so ALiBi costs two FMAs per score and the soft-cap an exp2, a
+    // reciprocal and two more VALU operations:
+    //   u = 2 log2e t / cap, tanh = 1 - 2/(2^u + 1), x = log2e cap tanh.
+    template <int BIAS, bool CAP>
+    __device__ __forceinline__ void score_mod_tile(int k0) {
+        const float c_s = CAP ? a.scale * (2.0f * kLog2e) * a.inv_softcap : a.scale_log2;
+        const float c_b = CAP ? (2.0f * kLog2e) * a.inv_softcap : kLog2e;
+        const float cap_hi = a.softcap * kLog2e, cap_m2 = -2.0f * a.softcap * kLog2e;
+        const float sl = slope * c_b;
+        const float base = sl * (float)(k0 + 8 * g - my_q);
+        float bvals[BN / 2];
+        if (BIAS == BIAS_DENSE) {
+            const float* br = bias_row + k0 + 8 * g;
+            if (k0 + BN <= a.N) {
+#pragma unroll
+                for (int q4 = 0; q4 < BN / 8; ++q4) {
+                    const f32x4 v = *(const f32x4*)(br + 16 * (q4 >> 1) + 4 * (q4 & 1));
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) bvals[4 * q4 + t] = v[t];
+                }
+            } else {
+#pragma unroll
+                for (int sb = 0; sb < BN / 32; ++sb)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        bvals[16 * sb + e] = bias_row[min(k0 + 8 * g + tile_pos(sb, e), a.N - 1)];
+            }
+        }
+#pragma unroll
+        for (int sb = 0; sb < BN / 32; ++sb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                float u;
+                if (BIAS == BIAS_ALIBI)
+                    u = __builtin_fmaf(s[sb][e], c_s, __builtin_fmaf(sl, (float)tile_pos(sb, e), base));
+                else if (BIAS == BIAS_DENSE)
+                    u = __builtin_fmaf(s[sb][e], c_s, bvals[16 * sb + e] * c_b);
+                else
+                    u = s[sb][e] * c_s;
+                if (CAP)
+                    u = __builtin_fmaf(cap_m2, __builtin_amdgcn_rcpf(__builtin_amdgcn_exp2f(u) + 1.0f), cap_hi);
+                s[sb][e] = u;
+            }
+    }
+    __device__ __forceinline__ void general_scores(int k0) {
+        const bool cap = a.softcap > 0.0f;
+        if (a.bias_kind == BIAS_ALIBI) {
+            if (cap) score_mod_tile<BIAS_ALIBI, true>(k0);
+            else score_mod_tile<BIAS_ALIBI, false>(k0);
+        } else if (a.bias_kind == BIAS_DENSE) {
+            if (cap) score_mod_tile<BIAS_DENSE, true>(k0);
+            else score_mod_tile<BIAS_DENSE, false>(k0);
+        } else {
+            if (cap) score_mod_tile<BIAS_NONE, true>(k0);
+            else score_mod_tile<BIAS_NONE, false>(k0);
+        }
+    }
+
+    // Masked scores -> -inf. Causal / ragged end: key k0+8g+pos is valid iff
+    // pos < lim. With a block mask whose blocks cut the slice: per element.
+    __device__ __forceinline__ void apply_mask(int e_ent, int k0) {
+        if (LIST && !list_full(e_ent, wave)) {
+            // masked_out (attention.cpp:54-62) per element, branch-free: the
+            // bitmap bytes are read at clamped indices and combined by selects
+            const int qb = my_q / a.mask_qbs;
+            const bool row_ok = qb < a.mask_qb;
+            const uint8_t* mrow = a.mask + (int64_t)min(qb, a.mask_qb - 1) * a.mask_kb;
+            const int klim = a.causal ? min(a.N - 1, my_q) : a.N - 1;  // last valid key
+            unsigned char byte[BN / 2];
+            int kbs[BN / 2];
+#pragma unroll
+            for (int i = 0; i < BN / 2; ++i) {
+                kbs[i] = min(k0 + 8 * g + tile_pos(i >> 4, i & 15), a.N - 1) / a.mask_kbs;
+                byte[i] = mrow[min(kbs[i], a.mask_kb - 1)];
+            }
+#pragma unroll
+            for (int sb = 0; sb < BN / 32; ++sb)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int i = 16 * sb + e;
+                    const int kj = k0 + 8 * g + tile_pos(sb, e);
+                    const bool ok = row_ok & (kj <= klim) & (kbs[i] < a.mask_kb) & (byte[i] != 0);
+                    s[sb][e] = ok ? s[sb][e] : kNegInf;
+                }
+            return;
+        }
+        const int lim = (a.causal ? min(a.N, my_q + 1) : a.N) - k0 - 8 * g;
+#pragma unroll
+        for (int sb = 0; sb < BN / 32; ++sb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                if (tile_pos(sb, e) >= lim) s[sb][e] = kNegInf;
+    }
+
+    // Online softmax of the scores in s (tile step with entry e_ent): running
     // max with lazy rescale of O and l, probabilities packed into pf, row sum.
-    __device__ __forceinline__ void softmax(int it) {
-        const int kt = tile_of(it);
+    __device__ __forceinline__ void softmax(int e_ent) {
+        const int kt = tile_of(e_ent);
         const int k0 = kt * BN;
-        const bool need_mask = tile_needs_mask(it, kt);
+        const bool need_mask = tile_crosses(kt) || (LIST && !list_full(e_ent, wave));
         float mx = kNegInf;
-        if (!GENERAL && !need_mask) {
+        const bool raw = MOD == MOD_PLAIN && !need_mask;  // s still holds raw dot products
+        if (raw) {
             if (a.scale_log2 >= 0.0f) {
 #pragma unroll
                 for (int sb = 0; sb < BN / 32; ++sb)
@@ -425,21 +546,17 @@ struct Wave32 {
                 mx = mn * a.scale_log2;
             }
         } else {
-            const bool row_out = GENERAL && my_q >= a.M;
+            if (MOD == MOD_GENERAL) {
+                general_scores(k0);
+            } else {
+#pragma unroll
+                for (int sb = 0; sb < BN / 32; ++sb) s[sb] *= a.scale_log2;
+            }
+            if (need_mask) apply_mask(e_ent, k0);
 #pragma unroll
             for (int sb = 0; sb < BN / 32; ++sb)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int kj = k0 + 32 * sb + acc_pos(e, g);
-                    const bool msk = row_out || (need_mask && elem_masked(a, my_q, kj));
-                    float x = kNegInf;
-                    if (!msk) {
-                        x = GENERAL ? general_score(a, s[sb][e], my_q, kj, slope, bias_row)
-                                    : s[sb][e] * a.scale_log2;
-                    }
-                    s[sb][e] = x;
-                    mx = fmaxf(mx, x);
-                }
+                for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[sb][e]);
         }
         mx = half_swap_max(mx);
 
@@ -456,7 +573,7 @@ struct Wave32 {
         }
         const float m_use = (m_run == kNegInf) ? 0.0f : m_run;
 
-        if (!GENERAL && !need_mask) {
+        if (raw) {
 #pragma unroll
             for (int c = 0; c < BN / 16; ++c)
 #pragma unroll
@@ -516,7 +633,8 @@ struct Wave32 {
     }
 };
 
-// Tiles of the workgroup's query block: ntiles and the block-mask list.
+// Tile steps of the workgroup's query block: their number and, with a block
+// mask, the list of entries.
 __device__ __forceinline__ void tile_range(const FwdArgs& a, int qt, int block_m, int& ntiles,
                                            const int*& list) {
     list = nullptr;
@@ -535,7 +653,7 @@ constexpr int kPingPongBlockM = 256;
 
 template <typename T, int D>
 __global__ __launch_bounds__(kPingPongThreads) void flash_fwd_pingpong_kernel(FwdArgs a) {
-    using W = Wave32<T, D, false, kPingPongThreads>;
+    using W = Wave32<T, D, MOD_PLAIN, false, kPingPongThreads>;
     using L = typename W::L;
     constexpr int kStages = 3;
     __shared__ __attribute__((aligned(16))) unsigned char smem[kStages * L::STAGE];
@@ -553,9 +671,9 @@ __global__ __launch_bounds__(kPingPongThreads) void flash_fwd_pingpong_kernel(Fw
     auto matrix_phase = [&](int it) {
         __builtin_amdgcn_s_setprio(1);
         if (it + 1 < ntiles) w.store_tile(stage_next);
-        if (it + 2 < ntiles) w.load_tile(w.tile_of(it + 2));
-        if (it > 0 && w.tile_active(w.tile_of(it - 1))) w.pv(stage_prev);
-        if (it < ntiles && w.tile_active(w.tile_of(it))) w.qk(stage_cur);
+        if (it + 2 < ntiles) w.load_tile(it + 2);
+        if (it > 0 && w.tile_active(it - 1)) w.pv(stage_prev);
+        if (it < ntiles && w.tile_active(it)) w.qk(stage_cur);
         const int t = stage_prev;
         stage_prev = stage_cur;
         stage_cur = stage_next;
@@ -563,13 +681,14 @@ __global__ __launch_bounds__(kPingPongThreads) void flash_fwd_pingpong_kernel(Fw
     };
     auto softmax_phase = [&](int it) {
         __builtin_amdgcn_s_setprio(0);
-        if (w.tile_active(w.tile_of(it))) w.softmax(it);
+        if (w.tile_active(it)) w.softmax(it);
     };
 
+    if (ntiles > 0) w.load_tile(0);
+    wait_vm_loads();
     if (ntiles > 0) {
-        w.load_tile(w.tile_of(0));
         w.store_tile(0);
-        if (ntiles > 1) w.load_tile(w.tile_of(1));
+        if (ntiles > 1) w.load_tile(1);
     }
     __syncthreads();
     if (group == 1) __syncthreads();  // group 1 runs one phase behind
@@ -586,11 +705,17 @@ __global__ __launch_bounds__(kPingPongThreads) void flash_fwd_pingpong_kernel(Fw
     w.store_output();
 }
 
-template <typename T, int D, bool GENERAL, int NWAVES>
+// All wavefronts run S, softmax and PV of a tile step between two barriers;
+// double-buffered LDS. Tile it+1 is stored to LDS at the end of step it, and
+// tile it+2 is loaded into registers right after, so its global latency is
+// hidden behind a whole step. With a list, entries are loaded three steps
+// ahead of their use.
+template <typename T, int D, int MOD, bool LIST, int NWAVES>
 __global__ __launch_bounds__(NWAVES * 64, 8 / NWAVES) void flash_fwd_lockstep_kernel(FwdArgs a) {
     constexpr int NTHREADS = NWAVES * 64;
     constexpr int BLOCK_M = NWAVES * kQueriesPerWave;
-    using W = Wave32<T, D, GENERAL, NTHREADS>;
+    static_assert(!LIST || NWAVES <= kListSlices, "list entries carry one bit per wavefront");
+    using W = Wave32<T, D, MOD, LIST, NTHREADS>;
     using L = typename W::L;
     __shared__ __attribute__((aligned(16))) unsigned char smem[2 * L::STAGE];
     const int wave = threadIdx.x >> 6;
@@ -600,20 +725,26 @@ __global__ __launch_bounds__(NWAVES * 64, 8 / NWAVES) void flash_fwd_lockstep_ke
     tile_range(a, qt, BLOCK_M, w.ntiles, w.list);
     const int ntiles = w.ntiles;
 
-    if (ntiles > 0) {
-        w.load_tile(w.tile_of(0));
-        w.store_tile(0);
-    }
+    int e_cur = ntiles > 0 ? w.entry(0) : 0;
+    int e_nxt = ntiles > 1 ? w.entry(1) : 0;
+    if (ntiles > 0) w.load_tile(w.tile_of(e_cur));
+    wait_vm_loads();
+    if (ntiles > 0) w.store_tile(0);
+    if (ntiles > 1) w.load_tile(w.tile_of(e_nxt));
+    int e_nn = ntiles > 2 ? w.entry(2) : 0;
     __syncthreads();
     for (int it = 0; it < ntiles; ++it) {
-        if (it + 1 < ntiles) w.load_tile(w.tile_of(it + 1));
         const int stage = (it & 1) * L::STAGE;
-        if (w.tile_active(w.tile_of(it))) {
+        if (w.tile_active(e_cur)) {
             w.qk(stage);
-            w.softmax(it);
+            w.softmax(e_cur);
             w.pv(stage);
         }
         if (it + 1 < ntiles) w.store_tile(((it + 1) & 1) * L::STAGE);
+        if (it + 2 < ntiles) w.load_tile(w.tile_of(e_nn));
+        e_cur = e_nxt;
+        e_nxt = e_nn;
+        e_nn = it + 3 < ntiles ? w.entry(it + 3) : 0;
         __syncthreads();
     }
     w.store_output();
@@ -706,13 +837,12 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a)
             *(f32x4*)(Vs + row * VSTR + 4 * cc) = vreg[u];
         }
     };
-    auto tile_at = [&](int it, bool& partial) -> int {
+    auto tile_at = [&](int it, int& ent) -> int {
         if (list != nullptr) {
-            const int e = list[it];
-            partial = (e & 1) != 0;
-            return e >> 1;
+            ent = list[it];
+            return list_tile(ent);
         }
-        partial = false;
+        ent = 0;
         return it;
     };
 
@@ -726,27 +856,28 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a)
         bias_row = a.bias + b * a.bias_sb + h * a.bias_sh + (int64_t)my_q * a.bias_sm;
 
     if (ntiles > 0) {
-        bool p0;
-        load_tile(tile_at(0, p0));
-        store_tile(0);
+        int e0;
+        load_tile(tile_at(0, e0));
     }
+    wait_vm_loads();
+    if (ntiles > 0) store_tile(0);
     __syncthreads();
 
     for (int it = 0; it < ntiles; ++it) {
-        bool partial;
-        const int kt = tile_at(it, partial);
+        int ent;
+        const int kt = tile_at(it, ent);
         if (it + 1 < ntiles) {
-            bool pn;
-            load_tile(tile_at(it + 1, pn));
+            int en;
+            load_tile(tile_at(it + 1, en));
         }
         const float* Ks = lds + (it & 1) * STAGE;
         const float* Vs = Ks + KTILE;
         const int k0 = kt * BN;
-        const bool active = !(a.causal && k0 > qw0 + kQueriesPerWave - 1);
+        const bool active = list != nullptr ? list_any(ent, wave)
+                                            : !(a.causal && k0 > qw0 + kQueriesPerWave - 1);
         if (active) {
-            const bool need_mask = list != nullptr
-                                       ? partial
-                                       : ((k0 + BN > a.N) || (a.causal && k0 + BN - 1 > qw0));
+            const bool need_mask = ((k0 + BN > a.N) || (a.causal && k0 + BN - 1 > qw0)) ||
+                                   (list != nullptr && !list_full(ent, wave));
             f32x16 s[1];
             s[0] = f32x16{};
             const float* krow = Ks + kappa(r) * KSTR + g * (D / 2);
@@ -815,11 +946,10 @@ static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
         case SCHED_PINGPONG:
             return launch(flash_fwd_pingpong_kernel<T, D>, kPingPongThreads, a, s);
         case SCHED_LOCKSTEP8:
-            return general_mod ? launch(flash_fwd_lockstep_kernel<T, D, true, 8>, 512, a, s)
-                               : launch(flash_fwd_lockstep_kernel<T, D, false, 8>, 512, a, s);
+            return launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8>, 512, a, s);
         default:
-            return general_mod ? launch(flash_fwd_lockstep_kernel<T, D, true, 4>, 256, a, s)
-                               : launch(flash_fwd_lockstep_kernel<T, D, false, 4>, 256, a, s);
+            return general_mod ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, true, 4>, 256, a, s)
+                               : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, true, 4>, 256, a, s);
     }
 }
 

@@ -41,7 +41,7 @@ struct FwdArgs {
     int mask_qbs, mask_kbs, mask_qb, mask_kb;
     // per-query-tile lists of key tiles (block mask only)
     const int* tile_counts;   // [num_q_tiles]
-    const int* tile_entries;  // [num_q_tiles, num_k_tiles], entry = kt*2 + partial
+    const int* tile_entries;  // [num_q_tiles, num_k_tiles], see list_entry()
     int num_q_tiles, num_k_tiles;
     // score_mod
     int bias_kind;
@@ -52,6 +52,19 @@ struct FwdArgs {
     float inv_softcap;
     int out_f32;        // 1: O is fp32, else O has the input dtype
 };
+
+// Block-mask tile list entry: the key tile index and, for each 32-row slice
+// w of the query tile (one wavefront each, at most kListSlices), bit w: the
+// slice holds a pair that the mask and the causal rule allow; bit 4+w: the
+// mask allows every pair of the slice (causal and ragged-end masking is still
+// applied element-wise by the attention kernel).
+constexpr int kListSlices = 4;
+__host__ __device__ inline int list_entry(int kt, unsigned any, unsigned full) {
+    return (kt << 8) | (int)((full & 15u) << 4) | (int)(any & 15u);
+}
+__host__ __device__ inline int list_tile(int e) { return e >> 8; }
+__host__ __device__ inline bool list_any(int e, int slice) { return ((e >> slice) & 1) != 0; }
+__host__ __device__ inline bool list_full(int e, int slice) { return ((e >> (4 + slice)) & 1) != 0; }
 
 struct TileListArgs {
     int M, N, block_m, block_n, causal;

@@ -146,48 +146,60 @@ hipError_t launch_rowwise(const FwdArgs& a, int dtype, hipStream_t s) {
 
 // ---------------------------------------------------------------------------
 // Block-mask tile lists: for each query tile of the flash kernel, the ordered
-// list of key tiles that hold at least one allowed (query, key) pair, with a
-// flag telling whether the tile also holds masked pairs (then the kernel masks
-// element-wise; otherwise it runs the unmasked fast path). Built before the
-// attention launch, so skipped tiles issue no loads at all. One wavefront per
-// query tile; the list is compacted in order with a ballot prefix count.
+// list of key tiles that hold at least one allowed (query, key) pair. Each
+// entry also says, per 32-row slice of the query tile (one wavefront of the
+// attention kernel), whether the slice has an allowed pair at all (else that
+// wavefront skips the tile) and whether the mask allows all of its pairs
+// (else it masks element-wise). Built before the attention launch, so skipped
+// tiles issue no loads at all. One wavefront per query tile; the list is
+// compacted in order with a ballot prefix count.
 namespace {
 
-__device__ int classify_tile(const TileListArgs& a, int q0, int q1, int k0, int k1, bool k_full) {
-    // [q0,q1) x [k0,k1) clipped to the problem; returns 0 empty, 1 full, 2 partial.
-    bool any = false, all = k_full;
+// Rows [q0,q1) x keys [k0,k1), already clipped to the problem. any: some pair
+// is allowed by the mask and by the causal rule; all: the mask allows every pair.
+__device__ void classify_slice(const TileListArgs& a, int q0, int q1, int k0, int k1, bool& any,
+                               bool& all) {
+    any = false;
+    all = true;
     const int qb0 = q0 / a.mask_qbs, qb1 = (q1 - 1) / a.mask_qbs;
     const int kb0 = k0 / a.mask_kbs, kb1 = (k1 - 1) / a.mask_kbs;
     for (int qb = qb0; qb <= qb1; ++qb) {
-        const int qs = max(q0, qb * a.mask_qbs), qe = min(q1, (qb + 1) * a.mask_qbs);
+        const int qe = min(q1, (qb + 1) * a.mask_qbs);
         for (int kb = kb0; kb <= kb1; ++kb) {
-            const int ks = max(k0, kb * a.mask_kbs), ke = min(k1, (kb + 1) * a.mask_kbs);
+            const int ks = max(k0, kb * a.mask_kbs);
             const bool allowed = qb < a.mask_qb && kb < a.mask_kb &&
                                  a.mask[(int64_t)qb * a.mask_kb + kb] != 0;
-            // causal: some key <= some query iff ks <= qe-1; every key <= every query iff ke-1 <= qs
+            // causal: some key of the block is <= some query of the block iff ks <= qe-1
             any = any || (allowed && (!a.causal || ks <= qe - 1));
-            all = all && allowed && (!a.causal || ke - 1 <= qs);
+            all = all && allowed;
         }
     }
-    if (!any) return 0;
-    return all ? 1 : 2;
 }
 
 __global__ __launch_bounds__(64) void tile_list_kernel(TileListArgs a) {
     const int qt = blockIdx.x, lane = threadIdx.x;
-    const int q0 = qt * a.block_m, q1 = min(a.M, q0 + a.block_m);
+    const int q0 = qt * a.block_m;
+    const int slices = a.block_m / 32;
     int count = 0;
     for (int base = 0; base < a.num_k_tiles; base += 64) {
         const int kt = base + lane;
-        int cls = 0;
+        unsigned any_bits = 0, full_bits = 0;
         if (kt < a.num_k_tiles) {
             const int k0 = kt * a.block_n;
             const int k1 = min(a.N, k0 + a.block_n);
-            cls = classify_tile(a, q0, q1, k0, k1, k0 + a.block_n <= a.N);
+            for (int w = 0; w < slices; ++w) {
+                const int s0 = q0 + 32 * w, s1 = min(a.M, s0 + 32);
+                if (s0 >= s1) continue;
+                bool any, all;
+                classify_slice(a, s0, s1, k0, k1, any, all);
+                any_bits |= (any ? 1u : 0u) << w;
+                full_bits |= (all ? 1u : 0u) << w;
+            }
         }
-        const unsigned long long bal = __ballot(cls != 0);
+        const unsigned long long bal = __ballot(any_bits != 0);
         const int pos = count + __popcll(bal & ((1ull << lane) - 1ull));
-        if (cls != 0) a.entries[(int64_t)qt * a.num_k_tiles + pos] = kt * 2 + (cls == 2 ? 1 : 0);
+        if (any_bits != 0)
+            a.entries[(int64_t)qt * a.num_k_tiles + pos] = list_entry(kt, any_bits, full_bits);
         count += __popcll(bal);
     }
     if (lane == 0) a.counts[qt] = count;
