@@ -41,6 +41,7 @@ struct Resolved {
     bool general_mod;    // bias or soft-cap present
     bool tile_list;      // block-mask tile lists are built
     int block_m, block_n, threads;
+    bool paired;         // causal query tiles run in pairs per workgroup
     int num_q_tiles, num_k_tiles;
 };
 
@@ -148,6 +149,7 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
         if (p->head_dim > 1024)
             return set_error(OFH_ERROR_UNSUPPORTED, "rowwise kernel supports head_dim <= 1024");
         r.tile_list = false;
+        r.paired = false;
         r.block_m = 1;
         r.block_n = 64;
         r.threads = 256;
@@ -157,10 +159,11 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
     }
     r.algorithm = OFH_ALGO_FLASH_MFMA;
     const ofh::MfmaTiles tiles =
-        ofh::flash_mfma_tiles(p->dtype, r.general_mod, p->mask_allowed != nullptr);
+        ofh::flash_mfma_tiles(p->dtype, r.general_mod, p->mask_allowed != nullptr, p->causal != 0);
     r.block_m = tiles.block_m;
     r.block_n = tiles.block_n;
     r.threads = tiles.threads;
+    r.paired = tiles.paired;
     r.num_q_tiles = (int)((p->query_tokens + r.block_m - 1) / r.block_m);
     r.num_k_tiles = (int)((p->key_tokens + r.block_n - 1) / r.block_n);
     r.tile_list = p->mask_allowed != nullptr;
@@ -444,7 +447,7 @@ int ofh_attention_launch_info(const ofh_attention_params* p, ofh_launch_info* in
         info->block_m = r.block_m;
         info->block_n = r.block_n;
         info->threads = r.threads;
-        info->workgroups = (int64_t)p->batch * p->heads * r.num_q_tiles;
+        info->workgroups = (int64_t)p->batch * p->heads * (r.paired ? (r.num_q_tiles + 1) / 2 : r.num_q_tiles);
         name = ofh::flash_mfma_kernel_name(p->dtype, (int)p->head_dim, r.general_mod, r.tile_list);
     } else {
         info->block_m = 1;

@@ -83,6 +83,37 @@ __device__ __forceinline__ void map_work(int id, int BH, int nqt, int causal, in
     qt = causal ? nqt - 1 - t : t;
 }
 
+// Causal attention without a block mask: workgroup id -> (flat head, query
+// tiles nqt-1-p and p). The heavy tile runs first, then the light one, so
+// every workgroup does the same number of tile steps (no tail of short
+// workgroups) and both tiles share the head's K/V in one XCD's L2. qt_b is
+// -1 when p is the middle tile of an odd count.
+__device__ __forceinline__ void map_work_pair(int id, int BH, int nqt, int& bh, int& qt_a, int& qt_b) {
+    const int np = (nqt + 1) / 2;
+    int p;
+    if ((BH & 7) == 0) {
+        const int xcd = id & 7, j = id >> 3;
+        const int hl = j / np;
+        p = j - hl * np;
+        bh = hl * 8 + xcd;
+    } else {
+        bh = id % BH;
+        p = id / BH;
+    }
+    qt_a = nqt - 1 - p;
+    qt_b = (p != qt_a) ? p : -1;
+}
+
+// Query tiles of this workgroup: one, or a causal pair (see map_work_pair).
+__device__ __forceinline__ int work_tiles(const FwdArgs& a, bool paired, int& bh, int (&qts)[2]) {
+    if (paired) {
+        map_work_pair(blockIdx.x, a.B * a.H, a.num_q_tiles, bh, qts[0], qts[1]);
+        return qts[1] >= 0 ? 2 : 1;
+    }
+    map_work(blockIdx.x, a.B * a.H, a.num_q_tiles, a.causal, bh, qts[0]);
+    return 1;
+}
+
 // masked_out (attention.cpp:54-62) plus the key-range bound of a ragged last tile.
 __device__ __forceinline__ bool elem_masked(const FwdArgs& a, int qi, int kj) {
     if (kj >= a.N) return true;
@@ -394,9 +425,25 @@ struct Wave32 {
         }
     }
 
-    // S^T = K Q^T for the tile in LDS stage `stage_off`
+    // S^T = K Q^T for the tile in LDS stage `stage_off`. With a score_mod
+    // (longer softmax) all K fragments are read before the first MFMA.
     __device__ __forceinline__ void qk(int stage_off) {
         const lds_u8* kb = (const lds_u8*)smem + stage_off + k_lane_off;
+        if (MOD == MOD_GENERAL) {
+            v8 kf[BN / 32][D / 16];
+#pragma unroll
+            for (int c = 0; c < D / 16; ++c)
+#pragma unroll
+                for (int sb = 0; sb < BN / 32; ++sb)
+                    kf[sb][c] = __builtin_bit_cast(v8, *(const lds_u32x4*)(kb + 32 * sb * L::KSTR + 32 * c));
+#pragma unroll
+            for (int sb = 0; sb < BN / 32; ++sb) s[sb] = f32x16{};
+#pragma unroll
+            for (int c = 0; c < D / 16; ++c)
+#pragma unroll
+                for (int sb = 0; sb < BN / 32; ++sb) s[sb] = M16::mma(kf[sb][c], qf[c], s[sb]);
+            return;
+        }
 #pragma unroll
         for (int sb = 0; sb < BN / 32; ++sb) {
             s[sb] = f32x16{};
@@ -409,21 +456,33 @@ struct Wave32 {
     }
 
     // O^T += V^T P^T for the tile in LDS stage `stage_off` (A operand from two
-    // transposed 4-key reads)
+    // transposed 4-key reads). With a score_mod all V^T fragments are read
+    // before the first MFMA.
     __device__ __forceinline__ void pv(int stage_off) {
         const lds_u8* vb = (const lds_u8*)smem + stage_off + v_lane_off;
+        auto vfrag = [&](int c, int db) {
+            const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_i16x4*)(vb + (16 * c) * L::VSTR + 64 * db));
+            const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_i16x4*)(vb + (16 * c + 4) * L::VSTR + 64 * db));
+            return __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        };
+        if (MOD == MOD_GENERAL) {
+            v8 vf[D / 32][BN / 16];
 #pragma unroll
-        for (int db = 0; db < D / 32; ++db) {
+            for (int c = 0; c < BN / 16; ++c)
 #pragma unroll
-            for (int c = 0; c < BN / 16; ++c) {
-                const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (lds_i16x4*)(vb + (16 * c) * L::VSTR + 64 * db));
-                const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (lds_i16x4*)(vb + (16 * c + 4) * L::VSTR + 64 * db));
-                const i16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                o[db] = M16::mma(__builtin_bit_cast(v8, both), pf[c], o[db]);
-            }
+                for (int db = 0; db < D / 32; ++db) vf[db][c] = vfrag(c, db);
+#pragma unroll
+            for (int c = 0; c < BN / 16; ++c)
+#pragma unroll
+                for (int db = 0; db < D / 32; ++db) o[db] = M16::mma(vf[db][c], pf[c], o[db]);
+            return;
         }
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+            for (int c = 0; c < BN / 16; ++c) o[db] = M16::mma(vfrag(c, db), pf[c], o[db]);
     }
 
     // Scores in log2 units with the call's score_mod: scale, then ALiBi
@@ -648,79 +707,19 @@ __device__ __forceinline__ void tile_range(const FwdArgs& a, int qt, int block_m
     }
 }
 
-constexpr int kPingPongThreads = 512;
-constexpr int kPingPongBlockM = 256;
-
-template <typename T, int D>
-__global__ __launch_bounds__(kPingPongThreads) void flash_fwd_pingpong_kernel(FwdArgs a) {
-    using W = Wave32<T, D, MOD_PLAIN, false, kPingPongThreads>;
-    using L = typename W::L;
-    constexpr int kStages = 3;
-    __shared__ __attribute__((aligned(16))) unsigned char smem[kStages * L::STAGE];
-    const int wave = threadIdx.x >> 6;
-    const int group = wave >> 2;  // waves w and w+4 share a SIMD
-    int bh, qt;
-    map_work(blockIdx.x, a.B * a.H, a.num_q_tiles, a.causal, bh, qt);
-    W w(a, smem, bh, qt * kPingPongBlockM, wave);
-    tile_range(a, qt, kPingPongBlockM, w.ntiles, w.list);
-    const int ntiles = w.ntiles;
-
-    // stage byte offsets of iterations it-1, it, it+1 (rotated every iteration)
-    int stage_prev = 2 * L::STAGE, stage_cur = 0, stage_next = L::STAGE;
-    // matrix phase of iteration `it`: O += P_{it-1} V_{it-1}; S_it = K_it Q^T
-    auto matrix_phase = [&](int it) {
-        __builtin_amdgcn_s_setprio(1);
-        if (it + 1 < ntiles) w.store_tile(stage_next);
-        if (it + 2 < ntiles) w.load_tile(it + 2);
-        if (it > 0 && w.tile_active(it - 1)) w.pv(stage_prev);
-        if (it < ntiles && w.tile_active(it)) w.qk(stage_cur);
-        const int t = stage_prev;
-        stage_prev = stage_cur;
-        stage_cur = stage_next;
-        stage_next = t;
-    };
-    auto softmax_phase = [&](int it) {
-        __builtin_amdgcn_s_setprio(0);
-        if (w.tile_active(it)) w.softmax(it);
-    };
-
-    if (ntiles > 0) w.load_tile(0);
-    wait_vm_loads();
-    if (ntiles > 0) {
-        w.store_tile(0);
-        if (ntiles > 1) w.load_tile(1);
-    }
-    __syncthreads();
-    if (group == 1) __syncthreads();  // group 1 runs one phase behind
-    for (int it = 0; it < ntiles; ++it) {
-        matrix_phase(it);
-        __syncthreads();
-        softmax_phase(it);
-        __syncthreads();
-    }
-    if (ntiles > 0) matrix_phase(ntiles);  // last O += P V
-    __syncthreads();
-    if (group == 0) __syncthreads();  // same barrier count for both groups
-    __builtin_amdgcn_s_setprio(0);
-    w.store_output();
-}
-
 // All wavefronts run S, softmax and PV of a tile step between two barriers;
 // double-buffered LDS. Tile it+1 is stored to LDS at the end of step it, and
 // tile it+2 is loaded into registers right after, so its global latency is
 // hidden behind a whole step. With a list, entries are loaded three steps
 // ahead of their use.
 template <typename T, int D, int MOD, bool LIST, int NWAVES>
-__global__ __launch_bounds__(NWAVES * 64, 8 / NWAVES) void flash_fwd_lockstep_kernel(FwdArgs a) {
+__device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* smem, int bh, int qt) {
     constexpr int NTHREADS = NWAVES * 64;
     constexpr int BLOCK_M = NWAVES * kQueriesPerWave;
     static_assert(!LIST || NWAVES <= kListSlices, "list entries carry one bit per wavefront");
     using W = Wave32<T, D, MOD, LIST, NTHREADS>;
     using L = typename W::L;
-    __shared__ __attribute__((aligned(16))) unsigned char smem[2 * L::STAGE];
-    const int wave = threadIdx.x >> 6;
-    int bh, qt;
-    map_work(blockIdx.x, a.B * a.H, a.num_q_tiles, a.causal, bh, qt);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     W w(a, smem, bh, qt * BLOCK_M, wave);
     tile_range(a, qt, BLOCK_M, w.ntiles, w.list);
     const int ntiles = w.ntiles;
@@ -750,6 +749,19 @@ __global__ __launch_bounds__(NWAVES * 64, 8 / NWAVES) void flash_fwd_lockstep_ke
     w.store_output();
 }
 
+template <typename T, int D, int MOD, bool LIST, int NWAVES, bool PAIRED>
+__global__ __launch_bounds__(NWAVES * 64, 8 / NWAVES) void flash_fwd_lockstep_kernel(FwdArgs a) {
+    using L = TileLayout<D>;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[2 * L::STAGE];
+    int bh, qts[2];
+    const int n = work_tiles(a, PAIRED, bh, qts);
+    lockstep_qtile<T, D, MOD, LIST, NWAVES>(a, smem, bh, qts[0]);
+    if (n > 1) {
+        __syncthreads();  // LDS stages are reused
+        lockstep_qtile<T, D, MOD, LIST, NWAVES>(a, smem, bh, qts[1]);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // fp32 inputs: v_mfma_f32_32x32x2_f32. Each MFMA consumes one element per lane
 // and operand, so K and V stay row-major in LDS (no transposition): the
@@ -775,7 +787,7 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a)
 
     __shared__ __attribute__((aligned(16))) float lds[2 * STAGE];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5, r = lane & 31;
 
     int bh, qt;
@@ -922,8 +934,8 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a)
 }
 
 template <typename K>
-hipError_t launch(K kernel, int threads, const FwdArgs& a, hipStream_t s) {
-    const int64_t grid = (int64_t)a.B * a.H * a.num_q_tiles;
+hipError_t launch(K kernel, int threads, const FwdArgs& a, hipStream_t s, bool paired = false) {
+    const int64_t grid = (int64_t)a.B * a.H * (paired ? (a.num_q_tiles + 1) / 2 : a.num_q_tiles);
     if (grid <= 0) return hipSuccess;
     hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(threads), 0, s, a);
     return hipGetLastError();
@@ -931,26 +943,27 @@ hipError_t launch(K kernel, int threads, const FwdArgs& a, hipStream_t s) {
 
 }  // namespace
 
-// 16-bit kernel schedule for a call: ping-pong for the plain scale without a
-// block-mask list, lockstep otherwise (4 wavefronts with a list, 8 without).
-enum Sched16 { SCHED_PINGPONG = 0, SCHED_LOCKSTEP8 = 1, SCHED_LOCKSTEP4 = 2 };
+// 16-bit kernel schedule for a call: 8 wavefronts (256 query rows) without a
+// block-mask list, 4 wavefronts (128 rows, finer skipping) with one.
+enum Sched16 { SCHED_LOCKSTEP8 = 0, SCHED_LOCKSTEP4 = 1 };
 
-static int sched16(bool general_mod, bool tile_list) {
-    if (tile_list) return SCHED_LOCKSTEP4;
-    return general_mod ? SCHED_LOCKSTEP8 : SCHED_PINGPONG;
-}
+// Causal calls without a block-mask list pair query tiles per workgroup.
+static bool pairs_causal_tiles(bool causal, bool tile_list) { return causal && !tile_list; }
+
+static int sched16(bool tile_list) { return tile_list ? SCHED_LOCKSTEP4 : SCHED_LOCKSTEP8; }
 
 template <typename T, int D>
 static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
-    switch (sched16(general_mod, a.tile_counts != nullptr)) {
-        case SCHED_PINGPONG:
-            return launch(flash_fwd_pingpong_kernel<T, D>, kPingPongThreads, a, s);
-        case SCHED_LOCKSTEP8:
-            return launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8>, 512, a, s);
-        default:
-            return general_mod ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, true, 4>, 256, a, s)
-                               : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, true, 4>, 256, a, s);
-    }
+    const bool list = a.tile_counts != nullptr;
+    const bool paired = pairs_causal_tiles(a.causal != 0, list);
+    if (list)
+        return general_mod ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, true, 4, false>, 256, a, s)
+                           : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, true, 4, false>, 256, a, s);
+    if (general_mod)
+        return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8, true>, 512, a, s, true)
+                      : launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8, false>, 512, a, s);
+    return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, true>, 512, a, s, true)
+                  : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, false>, 512, a, s);
 }
 
 hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipStream_t s) {
@@ -977,21 +990,25 @@ const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile
         {"flash_fwd_mfma32_kernel<64,plain>", "flash_fwd_mfma32_kernel<64,general>"},
         {"flash_fwd_mfma32_kernel<128,plain>", "flash_fwd_mfma32_kernel<128,general>"}};
     if (dtype == DT_F32) return f32names[D == 128][general_mod ? 1 : 0];
-    static const char* names[2][2][3] = {
-        {{"flash_fwd_pingpong_kernel<bf16,64>", "flash_fwd_lockstep_kernel<bf16,64,8w>", "flash_fwd_lockstep_kernel<bf16,64,4w>"},
-         {"flash_fwd_pingpong_kernel<bf16,128>", "flash_fwd_lockstep_kernel<bf16,128,8w>", "flash_fwd_lockstep_kernel<bf16,128,4w>"}},
-        {{"flash_fwd_pingpong_kernel<f16,64>", "flash_fwd_lockstep_kernel<f16,64,8w>", "flash_fwd_lockstep_kernel<f16,64,4w>"},
-         {"flash_fwd_pingpong_kernel<f16,128>", "flash_fwd_lockstep_kernel<f16,128,8w>", "flash_fwd_lockstep_kernel<f16,128,4w>"}}};
-    return names[dtype == DT_F16][D == 128][sched16(general_mod, tile_list)];
+    // [f16][D==128][score_mod][list]
+    static const char* names[2][2][2][2] = {
+        {{{"flash_fwd_lockstep_kernel<bf16,64,plain,8w>", "flash_fwd_lockstep_kernel<bf16,64,plain,list,4w>"},
+          {"flash_fwd_lockstep_kernel<bf16,64,mod,8w>", "flash_fwd_lockstep_kernel<bf16,64,mod,list,4w>"}},
+         {{"flash_fwd_lockstep_kernel<bf16,128,plain,8w>", "flash_fwd_lockstep_kernel<bf16,128,plain,list,4w>"},
+          {"flash_fwd_lockstep_kernel<bf16,128,mod,8w>", "flash_fwd_lockstep_kernel<bf16,128,mod,list,4w>"}}},
+        {{{"flash_fwd_lockstep_kernel<f16,64,plain,8w>", "flash_fwd_lockstep_kernel<f16,64,plain,list,4w>"},
+          {"flash_fwd_lockstep_kernel<f16,64,mod,8w>", "flash_fwd_lockstep_kernel<f16,64,mod,list,4w>"}},
+         {{"flash_fwd_lockstep_kernel<f16,128,plain,8w>", "flash_fwd_lockstep_kernel<f16,128,plain,list,4w>"},
+          {"flash_fwd_lockstep_kernel<f16,128,mod,8w>", "flash_fwd_lockstep_kernel<f16,128,mod,list,4w>"}}}};
+    return names[dtype == DT_F16][D == 128][general_mod ? 1 : 0][tile_list ? 1 : 0];
 }
 
-MfmaTiles flash_mfma_tiles(int dtype, bool general_mod, bool tile_list) {
-    if (dtype == DT_F32) return MfmaTiles{kBlockM32, kBlockNF32, kThreads32};
-    switch (sched16(general_mod, tile_list)) {
-        case SCHED_PINGPONG: return MfmaTiles{kPingPongBlockM, kBlockN16, kPingPongThreads};
-        case SCHED_LOCKSTEP8: return MfmaTiles{256, kBlockN16, 512};
-        default: return MfmaTiles{128, kBlockN16, 256};
-    }
+MfmaTiles flash_mfma_tiles(int dtype, bool general_mod, bool tile_list, bool causal) {
+    (void)general_mod;
+    if (dtype == DT_F32) return MfmaTiles{kBlockM32, kBlockNF32, kThreads32, false};
+    const bool paired = pairs_causal_tiles(causal, tile_list);
+    if (sched16(tile_list) == SCHED_LOCKSTEP4) return MfmaTiles{128, kBlockN16, 256, paired};
+    return MfmaTiles{256, kBlockN16, 512, paired};
 }
 
 }  // namespace ofh

@@ -15,9 +15,10 @@ enum Bias : int { BIAS_NONE = 0, BIAS_ALIBI = 1, BIAS_DENSE = 2 };
 constexpr int kQueriesPerWave = 32;
 
 struct MfmaTiles {
-    int block_m;  // query rows per workgroup
+    int block_m;  // query rows per query tile
     int block_n;  // keys per K/V tile
     int threads;  // threads per workgroup
+    bool paired;  // each workgroup runs query tiles nqt-1-p and p (causal)
 };
 
 // Everything a forward kernel needs, passed by value. Pointers are device
@@ -82,6 +83,6 @@ hipError_t launch_tile_lists(const TileListArgs& a, hipStream_t s);
 
 const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile_list);
 // Workgroup tiling of the MFMA kernel for a dtype.
-MfmaTiles flash_mfma_tiles(int dtype, bool general_mod, bool tile_list);
+MfmaTiles flash_mfma_tiles(int dtype, bool general_mod, bool tile_list, bool causal);
 
 }  // namespace ofh

@@ -104,14 +104,14 @@ def test_null_pointers_rejected_before_any_device_work(ofh):
 def test_kernel_choice(ofh):
     F = ofh
     cases = [
-        (dict(dtype=F.DTYPE_BF16, head_dim=128), "flash_fwd_pingpong_kernel<bf16,128>"),
-        (dict(dtype=F.DTYPE_F16, head_dim=64), "flash_fwd_pingpong_kernel<f16,64>"),
+        (dict(dtype=F.DTYPE_BF16, head_dim=128), "flash_fwd_lockstep_kernel<bf16,128,plain,8w>"),
+        (dict(dtype=F.DTYPE_F16, head_dim=64), "flash_fwd_lockstep_kernel<f16,64,plain,8w>"),
         (dict(dtype=F.DTYPE_F32, head_dim=64), "flash_fwd_mfma32_kernel<64,plain>"),
         (dict(dtype=F.DTYPE_BF16, head_dim=128, softcap=50.0),
-         "flash_fwd_lockstep_kernel<bf16,128,8w>"),
+         "flash_fwd_lockstep_kernel<bf16,128,mod,8w>"),
         (dict(dtype=F.DTYPE_F16, head_dim=64, mask_allowed=16, mask_query_block_size=64,
               mask_key_block_size=64, mask_query_blocks=4, mask_key_blocks=4),
-         "flash_fwd_lockstep_kernel<f16,64,4w>"),
+         "flash_fwd_lockstep_kernel<f16,64,plain,list,4w>"),
         (dict(dtype=F.DTYPE_BF16, head_dim=96), "rowwise_fwd_kernel"),
         (dict(dtype=F.DTYPE_BF16, head_dim=64, value_dim=128), "rowwise_fwd_kernel"),
         (dict(dtype=F.DTYPE_F32, head_dim=64, algorithm=F.ALGO_ROWWISE), "rowwise_fwd_kernel"),
@@ -122,7 +122,10 @@ def test_kernel_choice(ofh):
         info = F.launch_info(F.make_params(2, 3, 300, 200, D, Dv, **kw))
         assert info.kernel_name.decode() == name
     info = F.launch_info(F.make_params(4, 32, 4096, 4096, 128, dtype=F.DTYPE_BF16, causal=True))
-    assert info.workgroups == 4 * 32 * 16 and info.block_m == 256 and info.threads == 512
+    # causal: query tiles nqt-1-p and p share a workgroup
+    assert info.workgroups == 4 * 32 * 8 and info.block_m == 256 and info.threads == 512
+    info = F.launch_info(F.make_params(4, 32, 4096, 4096, 128, dtype=F.DTYPE_BF16))
+    assert info.workgroups == 4 * 32 * 16
 
 
 def test_useful_flops_match_workloads(ofh):
