@@ -555,22 +555,24 @@ struct Wave32 {
             const bool row_ok = qb < a.mask_qb;
             const uint8_t* mrow = a.mask + (int64_t)min(qb, a.mask_qb - 1) * a.mask_kb;
             const int klim = a.causal ? min(a.N - 1, my_q) : a.N - 1;  // last valid key
-            unsigned char byte[BN / 2];
-            int kbs[BN / 2];
+            // 8 consecutive keys at a time: their bitmap bytes are loaded together
 #pragma unroll
-            for (int i = 0; i < BN / 2; ++i) {
-                kbs[i] = min(k0 + 8 * g + tile_pos(i >> 4, i & 15), a.N - 1) / a.mask_kbs;
-                byte[i] = mrow[min(kbs[i], a.mask_kb - 1)];
-            }
+            for (int q8 = 0; q8 < BN / 16; ++q8) {
+                const int sb = q8 >> 1, e0 = 8 * (q8 & 1);
+                unsigned char byte[8];
+                int kbs[8];
 #pragma unroll
-            for (int sb = 0; sb < BN / 32; ++sb)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int i = 16 * sb + e;
-                    const int kj = k0 + 8 * g + tile_pos(sb, e);
-                    const bool ok = row_ok & (kj <= klim) & (kbs[i] < a.mask_kb) & (byte[i] != 0);
-                    s[sb][e] = ok ? s[sb][e] : kNegInf;
+                for (int t = 0; t < 8; ++t) {
+                    kbs[t] = min(k0 + 8 * g + tile_pos(sb, e0 + t), a.N - 1) / a.mask_kbs;
+                    byte[t] = mrow[min(kbs[t], a.mask_kb - 1)];
                 }
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const int kj = k0 + 8 * g + tile_pos(sb, e0 + t);
+                    const bool ok = row_ok & (kj <= klim) & (kbs[t] < a.mask_kb) & (byte[t] != 0);
+                    s[sb][e0 + t] = ok ? s[sb][e0 + t] : kNegInf;
+                }
+            }
             return;
         }
         const int lim = (a.causal ? min(a.N, my_q + 1) : a.N) - k0 - 8 * g;
