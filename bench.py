@@ -18,6 +18,7 @@ from __future__ import annotations
 import argparse
 import ctypes
 import json
+import math
 import os
 import sys
 import time
@@ -120,11 +121,30 @@ def cpu_baseline(w, threads: int, nheads: int, min_seconds: float = 10.0):
         if dt >= min_seconds or passes >= 64:
             break
     flops = 4.0 * w.head_dim * w.useful_pairs_per_head() * nheads * passes
+
+    def timed_rate(n_heads, n_threads, qb, kb, seconds):
+        reps, t_start = 0, time.perf_counter()
+        while True:
+            hs = np.arange(n_heads)
+            if kind == "reference":
+                O.ref_flash_heads(q, k, v, prob, hs, qb, kb, threads=n_threads)
+            else:
+                O.flash_heads(q, k, v, prob, hs, qb, kb, threads=n_threads)
+            reps += 1
+            el = time.perf_counter() - t_start
+            if el >= seconds or reps >= 64:
+                return 4.0 * w.head_dim * w.useful_pairs_per_head() * n_heads * reps / el / 1e12
+
+    # one thread on one head, and the TensorFlow op's default 16x32 tiles on all threads
+    one_thread = timed_rate(1, 1, q_bs, k_bs, min_seconds / 4)
+    tf_tiles = timed_rate(nheads, threads, 16, 32, min_seconds / 4)
     note = "" if kind == "reference" else " (oracle restatement: the reference has no soft-cap)" if w.softcap else ""
     return {
         "value": flops / dt / 1e12,
         "unit": "TFLOP/s",
         "cores": threads,
+        "value_1_thread": one_thread,
+        "value_tiles_16x32": tf_tiles,
         "kind": kind,
         "sample": (f"{nheads} of {w.batch * w.heads} heads of {w.name}, fp32 on {w.dtype}-rounded "
                    f"inputs, tiles {q_bs}x{k_bs}, {nheads} heads on {threads} threads, {passes} passes, "
@@ -194,6 +214,10 @@ def main() -> int:
     per_launch = [events[i].elapsed_time(events[i + 1]) for i in range(args.steps)]
     ms = events[0].elapsed_time(events[-1]) / args.steps
     avg_launch_ms = sum(per_launch) / len(per_launch)
+    srt = sorted(per_launch)
+
+    def pct(p):  # nearest-rank percentile
+        return srt[min(len(srt) - 1, max(0, math.ceil(p * len(srt)) - 1))]
 
     flops = w.useful_flops()
     value = flops / (ms * 1e-3) / 1e12
@@ -222,6 +246,9 @@ def main() -> int:
             "useful_gflop": round(flops / 1e9, 3),
         },
         "pct_bf16_peak": round(100.0 * value / C.PEAK_TFLOPS["bf16"], 2),
+        "launch_ms": {"mean": round(avg_launch_ms, 5), "median": round(pct(0.5), 5),
+                      "p10": round(pct(0.1), 5), "p90": round(pct(0.9), 5),
+                      "min": round(srt[0], 5), "max": round(srt[-1], 5)},
         "wall_s_timed": round(wall, 4),
         "roofline": {
             "bound": "mfma",
