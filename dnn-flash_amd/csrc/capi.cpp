@@ -485,6 +485,80 @@ int ofh_attention_useful_flops(const ofh_attention_params* p, double* flops) {
     return OFH_SUCCESS;
 }
 
+void ofh_qk_score_params_init(ofh_qk_score_params* p) {
+    if (p == nullptr) return;
+    std::memset(p, 0, sizeof(*p));
+    p->struct_size = sizeof(*p);
+    p->batch = 1;
+    p->dtype = OFH_DTYPE_F32;
+    p->scale = 1.0f;
+    p->algorithm = OFH_QK_AUTO;
+}
+
+int ofh_qk_score_tile(const ofh_qk_score_params* p, const void* q, const void* k, float* score,
+                      void* stream) {
+    if (p == nullptr) return set_error(OFH_ERROR_INVALID_ARGUMENT, "params must be non-null");
+    if (p->struct_size != sizeof(*p))
+        return set_error(OFH_ERROR_INVALID_ARGUMENT,
+                         "ofh_qk_score_params.struct_size mismatch (call ofh_qk_score_params_init)");
+    if (p->m <= 0 || p->n <= 0 || p->k <= 0)
+        return set_error(OFH_ERROR_INVALID_ARGUMENT, "QK score tile dimensions must be non-zero");
+    if (q == nullptr || k == nullptr || score == nullptr)
+        return set_error(OFH_ERROR_INVALID_ARGUMENT, "QK score tile pointers must be non-null");
+    if (p->batch <= 0) return set_error(OFH_ERROR_INVALID_ARGUMENT, "QK score tile batch must be positive");
+    const int64_t strides[] = {p->a_stride_m, p->a_stride_k, p->a_stride_batch, p->b_stride_k,
+                               p->b_stride_n, p->b_stride_batch, p->c_stride_m, p->c_stride_n,
+                               p->c_stride_batch, p->bias_stride_m, p->bias_stride_n,
+                               p->bias_stride_batch};
+    for (int64_t st : strides)
+        if (st < 0) return set_error(OFH_ERROR_INVALID_ARGUMENT, "QK score tile strides must be non-negative");
+    if (p->dtype != OFH_DTYPE_F32 && p->dtype != OFH_DTYPE_BF16 && p->dtype != OFH_DTYPE_F16)
+        return set_error(OFH_ERROR_INVALID_ARGUMENT, "unknown dtype");
+    if (!(std::isfinite(p->softcap) && p->softcap >= 0.0f))
+        return set_error(OFH_ERROR_INVALID_ARGUMENT, "softcap must be finite and >= 0");
+    if (p->algorithm != OFH_QK_AUTO && p->algorithm != OFH_QK_EXACT && p->algorithm != OFH_QK_MFMA)
+        return set_error(OFH_ERROR_INVALID_ARGUMENT, "unknown algorithm");
+    // Grid: x over 32-column blocks, y over 32-row blocks (at most 65535).
+    if ((p->m + 31) / 32 > 65535 || (p->n + 31) / 32 > std::numeric_limits<int32_t>::max())
+        return set_error(OFH_ERROR_UNSUPPORTED, "QK score tile exceeds the grid range");
+
+    ofh::QkScoreArgs a{};
+    a.batch = p->batch;
+    a.M = p->m;
+    a.N = p->n;
+    a.K = p->k;
+    a.q = q;
+    a.k = k;
+    a.c = score;
+    a.a_sm = p->a_stride_m;
+    a.a_sk = p->a_stride_k;
+    a.a_sb = p->a_stride_batch;
+    a.b_sk = p->b_stride_k;
+    a.b_sn = p->b_stride_n;
+    a.b_sb = p->b_stride_batch;
+    a.c_sm = p->c_stride_m;
+    a.c_sn = p->c_stride_n;
+    a.c_sb = p->c_stride_batch;
+    a.has_scale = p->has_scale != 0;
+    a.scale = p->scale;
+    a.bias = p->bias;
+    a.bias_sm = p->bias_stride_m;
+    a.bias_sn = p->bias_stride_n;
+    a.bias_sb = p->bias_stride_batch;
+    a.softcap = p->softcap;
+
+    const bool mfma_ok = ofh::qk_score_mfma_supported(a, p->dtype);
+    if (p->algorithm == OFH_QK_MFMA && !mfma_ok)
+        return set_error(OFH_ERROR_UNSUPPORTED,
+                         "MFMA QK score tile needs bf16/fp16 rows contiguous along k, 16-byte "
+                         "aligned, with k % 8 == 0");
+    const bool use_mfma = p->algorithm == OFH_QK_MFMA || (p->algorithm == OFH_QK_AUTO && mfma_ok);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    OFH_HIP_CHECK(use_mfma ? ofh::launch_qk_score_mfma(a, p->dtype, s)
+                           : ofh::launch_qk_score(a, p->dtype, s));
+    return OFH_SUCCESS;
+}
+
 const char* ofh_last_error(void) { return g_last_error.c_str(); }
 
 int ofh_abi_version(void) { return OFH_ABI_VERSION; }

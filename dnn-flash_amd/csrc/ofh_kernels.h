@@ -76,10 +76,31 @@ struct TileListArgs {
     int* entries;
 };
 
+// Batched strided fp32 score tile S = (Q K^T) * scale + bias (+ soft-cap).
+// Strides are in elements; b_* index the K^T view (kk, j); bias is fp32 or null.
+struct QkScoreArgs {
+    int64_t batch, M, N, K;
+    const void* q;
+    const void* k;
+    float* c;
+    int64_t a_sm, a_sk, a_sb;
+    int64_t b_sk, b_sn, b_sb;
+    int64_t c_sm, c_sn, c_sb;
+    int has_scale;
+    float scale;
+    const float* bias;
+    int64_t bias_sm, bias_sn, bias_sb;
+    float softcap;
+};
+
 // Launchers; each returns the hipError_t of the launch.
 hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipStream_t s);
 hipError_t launch_rowwise(const FwdArgs& a, int dtype, hipStream_t s);
 hipError_t launch_tile_lists(const TileListArgs& a, hipStream_t s);
+hipError_t launch_qk_score(const QkScoreArgs& a, int dtype, hipStream_t s);
+// Matrix-core score kernel for bf16/fp16 with unit k-strides and 16-byte rows.
+bool qk_score_mfma_supported(const QkScoreArgs& a, int dtype);
+hipError_t launch_qk_score_mfma(const QkScoreArgs& a, int dtype, hipStream_t s);
 
 const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile_list);
 // Workgroup tiling of the MFMA kernel for a dtype.

@@ -1,0 +1,260 @@
+// QK score tile with post-ops on the device: S = (Q K^T) * scale + bias
+// (+ soft-cap), for a batch of strided tiles.
+//
+// Follows the reference's QK score tile (src/onednn_flash/qk_score_tile.cpp:
+// 48-69 post-ops after matmul_tile_strided_inplace, whose reference kernel
+// sums over k sequentially in fp32, src/onednn_flash/tile_kernel.cpp:49-86).
+// Every product and every partial sum is rounded once, in the same order, so
+// fp32 results are bit-identical to the reference. 32x32 output blocks per
+// workgroup; Q and K^T chunks of 32 along k are staged through LDS as fp32.
+//
+// For bf16/fp16 inputs a matrix-core variant computes the same scores with
+// v_mfma_f32_32x32x16_{bf16,f16}: the products are exact in fp32 and only the
+// summation order differs from the sequential sum (error within k * 2^-24 *
+// sum_k |q k| per score). It needs rows contiguous along k and 16-byte aligned.
+
+#include "ofh_kernels.h"
+
+#include <algorithm>
+
+namespace ofh {
+namespace {
+
+constexpr int kQkTile = 32;
+constexpr int64_t kMaxGridZ = 65535;   // tiles per launch (grid z)
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T x) { return (float)x; }
+
+template <typename T>
+__global__ __launch_bounds__(256) void qk_score_kernel(QkScoreArgs a) {
+    // Products, sums, scale and bias are each rounded: no contraction to FMA.
+#pragma clang fp contract(off)
+    __shared__ float qs[kQkTile][kQkTile + 1];   // [row i][kk]
+    __shared__ float ks[kQkTile][kQkTile + 1];   // [kk][col j]
+    const int tid = threadIdx.x;
+    const int tx = tid & 31, ty = tid >> 5;      // column, row group (8 groups of 4 rows)
+    const int64_t bt = blockIdx.z;
+    const int64_t i0 = (int64_t)blockIdx.y * kQkTile, j0 = (int64_t)blockIdx.x * kQkTile;
+    const T* q = (const T*)a.q + bt * a.a_sb;
+    const T* k = (const T*)a.k + bt * a.b_sb;
+    const bool q_k_fast = a.a_sk <= a.a_sm, k_k_fast = a.b_sk <= a.b_sn;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int64_t k0 = 0; k0 < a.K; k0 += kQkTile) {
+        // Stage both chunks, zero outside the tile. Lanes walk whichever axis
+        // has the smaller stride so that row-major Q [m,k] and K [n,k] (both
+        // contiguous along k) are read with unit stride.
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int r = ty + 8 * u;
+            if (q_k_fast) {
+                const int64_t qi = i0 + r, qk = k0 + tx;
+                qs[r][tx] = (qi < a.M && qk < a.K) ? to_f32(q[qi * a.a_sm + qk * a.a_sk]) : 0.0f;
+            } else {
+                const int64_t qi = i0 + tx, qk = k0 + r;
+                qs[tx][r] = (qi < a.M && qk < a.K) ? to_f32(q[qi * a.a_sm + qk * a.a_sk]) : 0.0f;
+            }
+            if (k_k_fast) {
+                const int64_t kk = k0 + tx, kj = j0 + r;
+                ks[tx][r] = (kk < a.K && kj < a.N) ? to_f32(k[kk * a.b_sk + kj * a.b_sn]) : 0.0f;
+            } else {
+                const int64_t kk = k0 + r, kj = j0 + tx;
+                ks[r][tx] = (kk < a.K && kj < a.N) ? to_f32(k[kk * a.b_sk + kj * a.b_sn]) : 0.0f;
+            }
+        }
+        __syncthreads();
+        const int kn = (int)min((int64_t)kQkTile, a.K - k0);
+        for (int t = 0; t < kn; ++t) {
+            const float b = ks[t][tx];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[u] = acc[u] + qs[ty + 8 * u][t] * b;
+        }
+        __syncthreads();
+    }
+    const int64_t j = j0 + tx;
+    if (j >= a.N) return;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int64_t i = i0 + ty + 8 * u;
+        if (i >= a.M) continue;
+        float v = acc[u];
+        if (a.has_scale) v = v * a.scale;
+        if (a.bias != nullptr) v = v + a.bias[bt * a.bias_sb + i * a.bias_sm + j * a.bias_sn];
+        if (a.softcap > 0.0f) v = a.softcap * tanhf(v / a.softcap);
+        a.c[bt * a.c_sb + i * a.c_sm + j * a.c_sn] = v;
+    }
+}
+
+typedef __bf16 qk_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 qk_f16x8 __attribute__((ext_vector_type(8)));
+typedef float qk_f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned int qk_u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct QkMfma;
+template <>
+struct QkMfma<__bf16> {
+    static __device__ __forceinline__ qk_f32x16 run(qk_u32x4 a, qk_u32x4 b, qk_f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(qk_bf16x8, a),
+                                                       __builtin_bit_cast(qk_bf16x8, b), c, 0, 0, 0);
+    }
+};
+template <>
+struct QkMfma<_Float16> {
+    static __device__ __forceinline__ qk_f32x16 run(qk_u32x4 a, qk_u32x4 b, qk_f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(qk_f16x8, a),
+                                                      __builtin_bit_cast(qk_f16x8, b), c, 0, 0, 0);
+    }
+};
+
+// 128x128 score block per workgroup, 4 wavefronts of 64x64 (2x2 MFMA tiles of
+// 32x32). Operand lane layout of the 32x32x16 MFMA: lane l holds row (l & 31)
+// of Q (A) and row (l & 31) of K (B = K^T column), k elements 8*(l >> 5) .. +7
+// of the 16-wide step. Output element e of lane l is row 8*(e >> 2) +
+// 4*(l >> 5) + (e & 3), column l & 31 of the 32x32 tile.
+constexpr int kMfmaBlock = 128;
+
+template <typename T>
+__global__ __launch_bounds__(256) void qk_score_mfma_kernel(QkScoreArgs a) {
+    // Scale and bias are rounded separately, as the reference applies them.
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t bt = blockIdx.z;
+    const int64_t i0 = (int64_t)blockIdx.y * kMfmaBlock + (wave >> 1) * 64;
+    const int64_t j0 = (int64_t)blockIdx.x * kMfmaBlock + (wave & 1) * 64;
+    const T* q = (const T*)a.q + bt * a.a_sb;
+    const T* k = (const T*)a.k + bt * a.b_sb;
+    const int r = lane & 31, half = lane >> 5;
+    // Row pointers (clamped to row 0 when out of range; such lanes load zeros).
+    const T* qrow[2];
+    const T* krow[2];
+    bool qok[2], kok[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int64_t qi = i0 + 32 * t + r, kj = j0 + 32 * t + r;
+        qok[t] = qi < a.M;
+        kok[t] = kj < a.N;
+        qrow[t] = q + (qok[t] ? qi : 0) * a.a_sm + 8 * half;
+        krow[t] = k + (kok[t] ? kj : 0) * a.b_sn + 8 * half;
+    }
+    qk_f32x16 acc[2][2];
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[x][y][e] = 0.0f;
+    const qk_u32x4 zero = {0u, 0u, 0u, 0u};
+    for (int64_t k0 = 0; k0 < a.K; k0 += 16) {
+        const bool kin = k0 + 8 * half < a.K;   // K is a multiple of 8
+        qk_u32x4 qa[2], kb[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            qa[t] = (qok[t] && kin) ? *(const qk_u32x4*)(qrow[t] + k0) : zero;
+            kb[t] = (kok[t] && kin) ? *(const qk_u32x4*)(krow[t] + k0) : zero;
+        }
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+            for (int y = 0; y < 2; ++y) acc[x][y] = QkMfma<T>::run(qa[x], kb[y], acc[x][y]);
+    }
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+#pragma unroll
+        for (int y = 0; y < 2; ++y) {
+            const int64_t j = j0 + 32 * y + r;
+            if (j >= a.N) continue;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int64_t i = i0 + 32 * x + 8 * (e >> 2) + 4 * half + (e & 3);
+                if (i >= a.M) continue;
+                float v = acc[x][y][e];
+                if (a.has_scale) v = v * a.scale;
+                if (a.bias != nullptr)
+                    v = v + a.bias[bt * a.bias_sb + i * a.bias_sm + j * a.bias_sn];
+                if (a.softcap > 0.0f) v = a.softcap * tanhf(v / a.softcap);
+                a.c[bt * a.c_sb + i * a.c_sm + j * a.c_sn] = v;
+            }
+        }
+    }
+}
+
+}  // namespace
+
+bool qk_score_mfma_supported(const QkScoreArgs& a, int dtype) {
+    if (dtype != DT_BF16 && dtype != DT_F16) return false;
+    const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    return a.a_sk == 1 && a.b_sk == 1 && a.K % 8 == 0 && a.a_sm % 8 == 0 && a.b_sn % 8 == 0 &&
+           a.a_sb % 8 == 0 && a.b_sb % 8 == 0 && al16(a.q) && al16(a.k);
+}
+
+hipError_t launch_qk_score_mfma(const QkScoreArgs& a, int dtype, hipStream_t s) {
+    if (a.batch <= 0 || a.M <= 0 || a.N <= 0 || a.K <= 0) return hipSuccess;
+    if (!qk_score_mfma_supported(a, dtype)) return hipErrorInvalidValue;
+    for (int64_t b0 = 0; b0 < a.batch; b0 += kMaxGridZ) {
+        QkScoreArgs x = a;
+        x.batch = std::min<int64_t>(kMaxGridZ, a.batch - b0);
+        x.q = (const char*)a.q + b0 * a.a_sb * 2;
+        x.k = (const char*)a.k + b0 * a.b_sb * 2;
+        x.c = a.c + b0 * a.c_sb;
+        if (a.bias != nullptr) x.bias = a.bias + b0 * a.bias_sb;
+        const dim3 grid((unsigned)((a.N + kMfmaBlock - 1) / kMfmaBlock),
+                        (unsigned)((a.M + kMfmaBlock - 1) / kMfmaBlock), (unsigned)x.batch);
+        if (dtype == DT_BF16)
+            hipLaunchKernelGGL(qk_score_mfma_kernel<__bf16>, grid, dim3(256), 0, s, x);
+        else
+            hipLaunchKernelGGL(qk_score_mfma_kernel<_Float16>, grid, dim3(256), 0, s, x);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_qk_score(const QkScoreArgs& a, int dtype, hipStream_t s) {
+    if (a.batch <= 0 || a.M <= 0 || a.N <= 0 || a.K <= 0) return hipSuccess;
+    const size_t esz = dtype == DT_F32 ? 4 : 2;
+    for (int64_t b0 = 0; b0 < a.batch; b0 += kMaxGridZ) {
+        QkScoreArgs x = a;
+        x.batch = std::min<int64_t>(kMaxGridZ, a.batch - b0);
+        x.q = (const char*)a.q + b0 * a.a_sb * esz;
+        x.k = (const char*)a.k + b0 * a.b_sb * esz;
+        x.c = a.c + b0 * a.c_sb;
+        if (a.bias != nullptr) x.bias = a.bias + b0 * a.bias_sb;
+        const dim3 grid((unsigned)((a.N + kQkTile - 1) / kQkTile),
+                        (unsigned)((a.M + kQkTile - 1) / kQkTile), (unsigned)x.batch);
+        switch (dtype) {
+            case DT_F32: hipLaunchKernelGGL(qk_score_kernel<float>, grid, dim3(256), 0, s, x); break;
+            case DT_BF16: hipLaunchKernelGGL(qk_score_kernel<__bf16>, grid, dim3(256), 0, s, x); break;
+            case DT_F16: hipLaunchKernelGGL(qk_score_kernel<_Float16>, grid, dim3(256), 0, s, x); break;
+            default: return hipErrorInvalidValue;
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// Plain strided fp32 tile product (the tile-GEMM seam,
+// src/onednn_flash/tile_kernel.cpp:67-86): the score kernel with no post-ops.
+hipError_t launch_tile_gemm(const float* a, const float* b, float* c, int m, int n, int k,
+                            int64_t asm_, int64_t ask, int64_t bsk, int64_t bsn, int64_t csm,
+                            int64_t csn, hipStream_t s) {
+    QkScoreArgs x{};
+    x.batch = 1;
+    x.M = m;
+    x.N = n;
+    x.K = k;
+    x.q = a;
+    x.k = b;
+    x.c = c;
+    x.a_sm = asm_;
+    x.a_sk = ask;
+    x.b_sk = bsk;
+    x.b_sn = bsn;
+    x.c_sm = csm;
+    x.c_sn = csn;
+    return launch_qk_score(x, DT_F32, s);
+}
+
+}  // namespace ofh

@@ -29,6 +29,7 @@ OFH_ERROR_WORKSPACE_TOO_SMALL = 4
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 BIAS_NONE, BIAS_ALIBI, BIAS_DENSE = 0, 1, 2
 ALGO_AUTO, ALGO_FLASH_MFMA, ALGO_ROWWISE = 0, 1, 2
+QK_AUTO, QK_EXACT, QK_MFMA = 0, 1, 2
 
 # Every function the C header declares; tests check the library exports each.
 EXPORTED_SYMBOLS = (
@@ -38,6 +39,8 @@ EXPORTED_SYMBOLS = (
     "ofh_attention_fwd_host",
     "ofh_attention_launch_info",
     "ofh_attention_useful_flops",
+    "ofh_qk_score_params_init",
+    "ofh_qk_score_tile",
     "ofh_last_error",
     "ofh_abi_version",
 )
@@ -86,6 +89,34 @@ class LaunchInfo(ctypes.Structure):
     ]
 
 
+class QkScoreParams(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("batch", ctypes.c_int64),
+        ("m", ctypes.c_int64),
+        ("n", ctypes.c_int64),
+        ("k", ctypes.c_int64),
+        ("a_stride_m", ctypes.c_int64),
+        ("a_stride_k", ctypes.c_int64),
+        ("a_stride_batch", ctypes.c_int64),
+        ("b_stride_k", ctypes.c_int64),
+        ("b_stride_n", ctypes.c_int64),
+        ("b_stride_batch", ctypes.c_int64),
+        ("c_stride_m", ctypes.c_int64),
+        ("c_stride_n", ctypes.c_int64),
+        ("c_stride_batch", ctypes.c_int64),
+        ("dtype", ctypes.c_int32),
+        ("has_scale", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("bias", ctypes.c_void_p),
+        ("bias_stride_m", ctypes.c_int64),
+        ("bias_stride_n", ctypes.c_int64),
+        ("bias_stride_batch", ctypes.c_int64),
+        ("softcap", ctypes.c_float),
+        ("algorithm", ctypes.c_int32),
+    ]
+
+
 class OfhError(RuntimeError):
     def __init__(self, code: int, message: str):
         super().__init__(f"[ofh status {code}] {message}")
@@ -112,6 +143,11 @@ def lib() -> ctypes.CDLL:
         L.ofh_attention_fwd_host.argtypes = [P] + [ctypes.c_void_p] * 4
         L.ofh_attention_launch_info.argtypes = [P, ctypes.POINTER(LaunchInfo)]
         L.ofh_attention_useful_flops.argtypes = [P, ctypes.POINTER(ctypes.c_double)]
+        QP = ctypes.POINTER(QkScoreParams)
+        L.ofh_qk_score_params_init.argtypes = [QP]
+        L.ofh_qk_score_params_init.restype = None
+        L.ofh_qk_score_tile.argtypes = [QP] + [ctypes.c_void_p] * 4
+        L.ofh_qk_score_tile.restype = ctypes.c_int
         L.ofh_last_error.restype = ctypes.c_char_p
         L.ofh_last_error.argtypes = []
         L.ofh_abi_version.restype = ctypes.c_int
@@ -238,6 +274,46 @@ def attention_fwd(q, k, v, *, scale: float | None = None, causal: bool = False, 
     ws_ptr, ws_bytes = (0, 0) if workspace is None else (workspace.data_ptr(), workspace.numel() * workspace.element_size())
     check(lib().ofh_attention_fwd(ctypes.byref(p), q.data_ptr(), k.data_ptr(), v.data_ptr(),
                                   out.data_ptr(), ws_ptr or None, ws_bytes, stream))
+    return out
+
+
+def qk_score_tile(q, k, *, scale: float | None = None, bias=None, softcap: float = 0.0,
+                  out=None, algorithm: int = QK_AUTO, stream=None):
+    """Scores S = (Q K^T) * scale + bias for a batch of tiles on the device
+    (qk_score_tile_inplace, src/onednn_flash/qk_score_tile.cpp:353-418).
+    q: [T, M, D], k: [T, N, D] device tensors (f32/bf16/f16, any strides);
+    bias: f32 [T, M, N], [M, N] (shared by every tile) or None; scale None
+    means no scale post-op. Returns out, f32 [T, M, N]."""
+    torch = _torch()
+    T, M, D = q.shape
+    N = k.shape[1]
+    if k.shape[0] != T or k.shape[2] != D or k.dtype != q.dtype:
+        raise ValueError("k must be [T, N, D] with the dtype of q")
+    if out is None:
+        out = torch.empty((T, M, N), device=q.device, dtype=torch.float32)
+    p = QkScoreParams()
+    lib().ofh_qk_score_params_init(ctypes.byref(p))
+    p.batch, p.m, p.n, p.k = T, M, N, D
+    p.a_stride_batch, p.a_stride_m, p.a_stride_k = q.stride()
+    p.b_stride_batch, p.b_stride_n, p.b_stride_k = k.stride()
+    p.c_stride_batch, p.c_stride_m, p.c_stride_n = out.stride()
+    p.dtype = dtype_code(q.dtype)
+    if scale is not None:
+        p.has_scale, p.scale = 1, scale
+    if bias is not None:
+        if bias.dtype != torch.float32:
+            raise ValueError("bias must be float32")
+        p.bias = bias.data_ptr()
+        if bias.dim() == 2:
+            p.bias_stride_batch, (p.bias_stride_m, p.bias_stride_n) = 0, bias.stride()
+        else:
+            p.bias_stride_batch, p.bias_stride_m, p.bias_stride_n = bias.stride()
+    p.softcap = softcap
+    p.algorithm = algorithm
+    if stream is None:
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+    check(lib().ofh_qk_score_tile(ctypes.byref(p), q.data_ptr(), k.data_ptr(), out.data_ptr(),
+                                  stream))
     return out
 
 

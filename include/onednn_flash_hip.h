@@ -20,6 +20,8 @@
  *                                (src/onednn_flash/attention_workspace.cpp:5-20)
  *   OFH_ALGO_ROWWISE             standard_attention
  *                                (src/onednn_flash/attention.cpp:88-137)
+ *   ofh_qk_score_tile            qk_score_tile_inplace
+ *                                (src/onednn_flash/qk_score_tile.cpp:353-418)
  *   ofh_last_error               the what() text of the exceptions the reference
  *                                throws (std::invalid_argument / std::runtime_error)
  */
@@ -149,6 +151,54 @@ int ofh_attention_launch_info(const ofh_attention_params* p, ofh_launch_info* in
  * (2*(D+Dv)*pairs*B*H in general), counted exactly on the host from the mask.
  * The mask pointer must be a host pointer here. */
 int ofh_attention_useful_flops(const ofh_attention_params* p, double* flops);
+
+/* ---------------------------------------------------------------------------
+ * QK score tile with post-ops: S = (Q K^T) * scale + bias on the device, for a
+ * batch of independent strided tiles. Replaces qk_score_tile_inplace
+ * (src/onednn_flash/qk_score_tile.cpp:353-418, post-ops :48-69) on device
+ * buffers. Element (i, kk) of tile b of Q is q[b*a_stride_batch + i*a_stride_m
+ * + kk*a_stride_k]; K^T (the reference's B operand) element (kk, j) is
+ * k[b*b_stride_batch + kk*b_stride_k + j*b_stride_n] (row-major K [n,k]:
+ * b_stride_k = 1, b_stride_n = k); scores are fp32. Each score is the
+ * reference's sequential-k fp32 sum (one rounding per product and per add),
+ * then times scale, then plus bias (OFH_QK_EXACT): bit-exact with the
+ * reference for fp32 inputs, and with the fp32 upcast of bf16/fp16 inputs.
+ * OFH_QK_MFMA (bf16/fp16, rows contiguous along k, 16-byte aligned, k % 8 == 0)
+ * runs on the matrix cores: products are exact, the summation order differs
+ * (|error| <= k * 2^-24 * sum_k |q k| before scale and bias). AUTO picks MFMA
+ * for 16-bit inputs that meet its layout rule and EXACT otherwise. */
+typedef enum ofh_qk_algorithm {
+    OFH_QK_AUTO = 0,
+    OFH_QK_EXACT = 1,
+    OFH_QK_MFMA = 2
+} ofh_qk_algorithm;
+
+typedef struct ofh_qk_score_params {
+    uint32_t struct_size;
+    int64_t batch;                         /* number of tiles */
+    int64_t m, n, k;
+    int64_t a_stride_m, a_stride_k, a_stride_batch;
+    int64_t b_stride_k, b_stride_n, b_stride_batch;
+    int64_t c_stride_m, c_stride_n, c_stride_batch;
+    int32_t dtype;                         /* ofh_dtype of Q and K */
+    int32_t has_scale;
+    float scale;
+    const float* bias;                     /* device pointer or NULL */
+    int64_t bias_stride_m, bias_stride_n, bias_stride_batch;
+    float softcap;                         /* 0: off; else cap*tanh(s/cap) last */
+    int32_t algorithm;                     /* ofh_qk_algorithm */
+} ofh_qk_score_params;
+
+/* Defaults: one tile, fp32, AUTO, no scale (scale 1), no bias, sizes and
+ * strides zero. */
+void ofh_qk_score_params_init(ofh_qk_score_params* p);
+
+/* Stream-ordered; returns OFH_SUCCESS or an error code (ofh_last_error()).
+ * Errors: zero m, n or k -> "QK score tile dimensions must be non-zero";
+ * null q, k or score -> "QK score tile pointers must be non-null"
+ * (qk_score_tile.cpp:16-26). */
+int ofh_qk_score_tile(const ofh_qk_score_params* p, const void* q, const void* k, float* score,
+                      void* stream);
 
 /* Thread-local text of the last error on this thread ("" if none). */
 const char* ofh_last_error(void);

@@ -439,6 +439,30 @@ void oracle_f16_to_f32(const uint16_t* in, float* out, size_t n) {
     }
 }
 
+int oracle_qk_score_tile(const float* q, const float* k, float* score, const oracle_qk_shape* s,
+                         int has_scale, float scale, const float* bias, float softcap) {
+    if (s == nullptr) return fail("shape must be non-null");
+    if (s->m == 0 || s->n == 0 || s->k == 0) return fail("QK score tile dimensions must be non-zero");
+    if (q == nullptr || k == nullptr || score == nullptr)
+        return fail("QK score tile pointers must be non-null");
+    for (size_t b = 0; b < s->batch; ++b) {
+        const float* qb = q + b * s->a_sb;
+        const float* kb = k + b * s->b_sb;
+        float* cb = score + b * s->c_sb;
+        for (size_t i = 0; i < s->m; ++i) {
+            for (size_t j = 0; j < s->n; ++j) {
+                float sum = 0.0f;
+                for (size_t kk = 0; kk < s->k; ++kk) sum += qb[i * s->a_sm + kk * s->a_sk] * kb[kk * s->b_sk + j * s->b_sn];
+                if (has_scale) sum *= scale;
+                if (bias != nullptr) sum += bias[b * s->bias_sb + i * s->bias_sm + j * s->bias_sn];
+                if (softcap > 0.0f) sum = softcap * std::tanh(sum / softcap);
+                cb[i * s->c_sm + j * s->c_sn] = sum;
+            }
+        }
+    }
+    return 0;
+}
+
 uint64_t oracle_splitmix64(uint64_t x) {
     uint64_t z = x + 0x9E3779B97F4A7C15ull;
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;

@@ -15,6 +15,8 @@
  *                                   src/onednn_flash/tile_kernel.cpp:49-86
  *   - masked_out / BlockMask::allows / score_bias
  *                                   src/onednn_flash/attention.cpp:54-86
+ *   - the QK score tile with scale and bias post-ops
+ *                                   src/onednn_flash/qk_score_tile.cpp:48-69
  * and extends it with what the reference does not have:
  *   - a per-head ALiBi bias slope_h*(k-q) (the reference ScoreBiasFn has no head
  *     index, include/onednn_flash/attention.hpp:31),
@@ -98,6 +100,23 @@ void oracle_f16_to_f32(const uint16_t* in, float* out, size_t n);
 /* Counter-based N(mean, std) generator: element i depends only on (seed, i).
  * splitmix64 finaliser over (seed, i) -> two 53-bit uniforms -> Box-Muller
  * (cosine branch), computed in double, rounded to float. */
+/* QK score tile with post-ops over a batch of strided tiles, as
+ * qk_score_tile_inplace's reference path (src/onednn_flash/qk_score_tile.cpp:
+ * 48-69 after matmul_tile_reference_strided_inplace, tile_kernel.cpp:67-86):
+ *   s = sum_kk q[i,kk]*k[kk,j]  (fp32, kk ascending, one rounding per op)
+ *   s = s*scale (if has_scale);  s = s + bias[i,j] (if bias);
+ *   s = cap*tanh(s/cap) (if softcap > 0; an extension, not in the reference).
+ * Strides are in elements; q index b*a_sb + i*a_sm + kk*a_sk, k index
+ * b*b_sb + kk*b_sk + j*b_sn (the K^T view), score b*c_sb + i*c_sm + j*c_sn. */
+typedef struct oracle_qk_shape {
+    size_t batch, m, n, k;
+    size_t a_sm, a_sk, a_sb, b_sk, b_sn, b_sb, c_sm, c_sn, c_sb;
+    size_t bias_sm, bias_sn, bias_sb;
+} oracle_qk_shape;
+
+int oracle_qk_score_tile(const float* q, const float* k, float* score, const oracle_qk_shape* s,
+                         int has_scale, float scale, const float* bias, float softcap);
+
 void oracle_fill_normal(uint64_t seed, size_t n, float mean, float stddev, float* out,
                         int threads);
 uint64_t oracle_splitmix64(uint64_t x);

@@ -27,6 +27,12 @@ _c_u8_p = ctypes.POINTER(ctypes.c_uint8)
 _c_u16_p = ctypes.POINTER(ctypes.c_uint16)
 
 
+class _QkShape(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_size_t) for name in (
+        "batch", "m", "n", "k", "a_sm", "a_sk", "a_sb", "b_sk", "b_sn", "b_sb", "c_sm", "c_sn",
+        "c_sb", "bias_sm", "bias_sn", "bias_sb")]
+
+
 class _Params(ctypes.Structure):
     _fields_ = [
         ("batch", ctypes.c_size_t),
@@ -125,6 +131,10 @@ def lib() -> ctypes.CDLL:
             fn = getattr(L, name)
             fn.argtypes = args
             fn.restype = ctypes.c_int
+        L.oracle_qk_score_tile.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                           ctypes.POINTER(_QkShape), ctypes.c_int, ctypes.c_float,
+                                           ctypes.c_void_p, ctypes.c_float]
+        L.oracle_qk_score_tile.restype = ctypes.c_int
         L.oracle_f32_to_bf16.argtypes = [_c_float_p, _c_u16_p, ctypes.c_size_t]
         L.oracle_bf16_to_f32.argtypes = [_c_u16_p, _c_float_p, ctypes.c_size_t]
         L.oracle_f32_to_f16.argtypes = [_c_float_p, _c_u16_p, ctypes.c_size_t]
@@ -149,6 +159,39 @@ def _check(rc: int) -> None:
 
 def _f32(a) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _elem_strides(a: np.ndarray) -> tuple[int, ...]:
+    if a.dtype != np.float32 or any(st < 0 or st % 4 for st in a.strides):
+        raise ValueError("expected a float32 view with non-negative element strides")
+    return tuple(st // 4 for st in a.strides)
+
+
+def qk_score_tile(q, k, *, scale: float | None = None, bias=None, softcap: float = 0.0,
+                  out: np.ndarray | None = None) -> np.ndarray:
+    """Scores of a batch of tiles: q [T, M, D], k [T, N, D] float32 views (any
+    non-negative strides), bias float32 [T, M, N] or [M, N] (shared) or None;
+    scale None means no scale post-op. Sequential fp32 sums, then scale, then
+    bias (then soft-cap), as oracle_qk_score_tile. Returns float32 [T, M, N]
+    (or fills `out`, a float32 view of that shape)."""
+    T, M, D = q.shape
+    N = k.shape[1]
+    if out is None:
+        out = np.zeros((T, M, N), np.float32)
+    qs, ks, cs = _elem_strides(q), _elem_strides(k), _elem_strides(out)
+    sh = _QkShape(batch=T, m=M, n=N, k=D, a_sb=qs[0], a_sm=qs[1], a_sk=qs[2], b_sb=ks[0],
+                  b_sn=ks[1], b_sk=ks[2], c_sb=cs[0], c_sm=cs[1], c_sn=cs[2])
+    bias_ptr = None
+    if bias is not None:
+        bst = _elem_strides(bias)
+        if bias.ndim == 2:
+            bst = (0,) + bst
+        sh.bias_sb, sh.bias_sm, sh.bias_sn = bst
+        bias_ptr = bias.ctypes.data
+    _check(lib().oracle_qk_score_tile(q.ctypes.data, k.ctypes.data, out.ctypes.data,
+                                      ctypes.byref(sh), int(scale is not None),
+                                      1.0 if scale is None else scale, bias_ptr, softcap))
+    return out
 
 
 def standard_attention(q, k, v, prob: Problem) -> np.ndarray:
@@ -272,6 +315,9 @@ def ref() -> ctypes.CDLL:
                                                sz, sz, sz, sz, _c_float_p, _c_size_p, sz,
                                                ctypes.c_int])
         L.ref_flash_batched_heads.restype = ctypes.c_int
+        L.ref_qk_score_tile.argtypes = ([ctypes.c_void_p] * 3 + [sz] * 9 +
+                                        [ctypes.c_int, ctypes.c_float, ctypes.c_void_p, sz, sz])
+        L.ref_qk_score_tile.restype = ctypes.c_int
         _ref = L
     return _ref
 
@@ -313,4 +359,29 @@ def ref_flash_heads(q, k, v, prob: Problem, head_idx, q_bs: int, k_bs: int,
         h.ctypes.data_as(_c_size_p), len(h), threads)
     if rc != 0:
         raise ValueError(ref().ref_last_error().decode())
+    return out
+
+
+def ref_qk_score_tile(q, k, *, scale: float | None = None, bias=None,
+                      out: np.ndarray | None = None) -> np.ndarray:
+    """The reference's qk_score_tile_inplace (no-oneDNN plan) on each tile of
+    q [T, M, D], k [T, N, D] (float32 views), bias [T, M, N] / [M, N] / None."""
+    T, M, D = q.shape
+    N = k.shape[1]
+    if out is None:
+        out = np.zeros((T, M, N), np.float32)
+    for t in range(T):
+        qt, kt, ct = q[t], k[t], out[t]
+        qs, ks, cs = _elem_strides(qt), _elem_strides(kt), _elem_strides(ct)
+        bp, bsm, bsn = None, 0, 1
+        if bias is not None:
+            bt = bias if bias.ndim == 2 else bias[t]
+            bsm, bsn = _elem_strides(bt)
+            bp = bt.ctypes.data
+        rc = ref().ref_qk_score_tile(qt.ctypes.data, kt.ctypes.data, ct.ctypes.data, M, N, D,
+                                     qs[0], qs[1], ks[1], ks[0], cs[0], cs[1],
+                                     int(scale is not None), 1.0 if scale is None else scale,
+                                     bp, bsm, bsn)
+        if rc != 0:
+            raise ValueError(ref().ref_last_error().decode())
     return out

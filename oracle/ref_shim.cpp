@@ -16,6 +16,7 @@
 
 #include "onednn_flash/attention.hpp"
 #include "onednn_flash/batched_attention.hpp"
+#include "onednn_flash/qk_score_tile_internal.hpp"
 
 namespace {
 
@@ -147,6 +148,39 @@ int ref_flash_batched_heads(const float* q, const float* k, const float* v, floa
         }
     }
     return 0;
+}
+
+// qk_score_tile_inplace (src/onednn_flash/qk_score_tile.cpp:404-418) on one
+// strided fp32 tile, with the plan make_runtime_plan gives for a build without
+// oneDNN (the reference tile product plus reference post-ops). bias may be null.
+int ref_qk_score_tile(const float* q, const float* k, float* score, std::size_t m, std::size_t n,
+                      std::size_t kdim, std::size_t a_sm, std::size_t a_sk, std::size_t b_sk,
+                      std::size_t b_sn, std::size_t c_sm, std::size_t c_sn, int has_scale,
+                      float scale, const float* bias, std::size_t bias_sm, std::size_t bias_sn) {
+    return guarded([&]() {
+        onednn_flash::RuntimePlanInput in;
+        in.query_length = static_cast<int>(m);
+        in.key_length = static_cast<int>(n);
+        in.head_dim = static_cast<int>(kdim);
+        in.value_dim = static_cast<int>(kdim);
+        in.has_scale = has_scale != 0;
+        in.scale_value = scale;
+        if (bias != nullptr) {
+            in.requested_score_mod = has_scale ? onednn_flash::ScoreModKind::ScaleAdditiveBias
+                                               : onednn_flash::ScoreModKind::AdditiveBias;
+            in.requested_bias_kind = onednn_flash::BiasKind::SameShapeTile;
+        } else {
+            in.requested_score_mod = has_scale ? onednn_flash::ScoreModKind::Scale
+                                               : onednn_flash::ScoreModKind::None;
+        }
+        const auto plan = onednn_flash::make_runtime_plan(in, false, false);
+        onednn_flash::QkScoreTilePostOpsInput post_ops;
+        post_ops.additive_bias = bias;
+        post_ops.additive_bias_stride_m = bias_sm;
+        post_ops.additive_bias_stride_n = bias_sn;
+        const onednn_flash::StridedMatmulShape shape{m, n, kdim, a_sm, a_sk, b_sk, b_sn, c_sm, c_sn};
+        onednn_flash::qk_score_tile_inplace(q, k, score, shape, plan, post_ops);
+    });
 }
 
 }  // extern "C"

@@ -3,16 +3,22 @@
 // attention entry point against standard_attention on M=N=128, D=64, causal,
 // scale 1/8, inputs sin(0.013 i + {0.1, 1.3, 2.7}) * 0.25, max-abs <= 1e-5.
 // Also exercises the batched and raw-pointer entries, BlockMask, ScoreBiasFn,
-// per-head ALiBi, the tile-GEMM seam and the error contract. Exit code 0 = pass.
+// per-head ALiBi, the tile-GEMM seam and the error contract, and the QK score
+// tile with post-ops on the reference microbench's cases
+// (benchmarks/bench_qk_postops.cpp:186-231,441-447), bit for bit against its
+// inline fp32 loop (build with -ffp-contract=off). Exit code 0 = pass.
 
 #include <cmath>
 #include <cstdio>
+#include <cstring>
 #include <stdexcept>
 #include <vector>
 
 #include "onednn_flash/attention.hpp"
 #include "onednn_flash/backend.hpp"
 #include "onednn_flash/batched_attention.hpp"
+#include "onednn_flash/qk_score_tile_internal.hpp"
+#include "onednn_flash/runtime_plan.hpp"
 
 namespace of = onednn_flash;
 
@@ -38,6 +44,110 @@ static void expect_throw(Fn&& fn, const char* what) {
     } catch (...) {
     }
     expect(thrown, what, thrown ? 1.0 : 0.0);
+}
+
+// QK score tile: shapes x score cases x sync modes of the reference microbench.
+static void qk_score_checks() {
+    struct Shape { int batch, heads; std::size_t m, n, d; };
+    struct Case { const char* name; of::ScoreModKind kind; bool has_scale; bool has_bias; };
+    const Shape shapes[] = {{1, 1, 64, 64, 32}, {1, 1, 128, 128, 64}, {1, 4, 128, 128, 64}};
+    const Case cases[] = {{"none", of::ScoreModKind::None, false, false},
+                          {"scale", of::ScoreModKind::Scale, true, false},
+                          {"scale_additive_bias", of::ScoreModKind::ScaleAdditiveBias, true, true}};
+    bool all_exact = true, all_hip = true;
+    for (const Shape& sh : shapes) {
+        const std::size_t tiles = static_cast<std::size_t>(sh.batch) * sh.heads;
+        std::vector<float> q(tiles * sh.m * sh.d), k(tiles * sh.n * sh.d), bias(tiles * sh.m * sh.n);
+        for (std::size_t i = 0; i < q.size(); ++i) q[i] = std::sin(static_cast<float>(i) * 0.017f + 0.1f) * 0.25f;
+        for (std::size_t i = 0; i < k.size(); ++i) k[i] = std::sin(static_cast<float>(i) * 0.017f + 0.7f) * 0.25f;
+        for (std::size_t i = 0; i < bias.size(); ++i) bias[i] = std::sin(static_cast<float>(i) * 0.017f + 1.3f) * 0.25f;
+        for (const Case& c : cases) {
+            of::RuntimePlanInput in;
+            in.batch = sh.batch;
+            in.heads = sh.heads;
+            in.query_length = static_cast<int>(sh.m);
+            in.key_length = static_cast<int>(sh.n);
+            in.head_dim = static_cast<int>(sh.d);
+            in.value_dim = static_cast<int>(sh.d);
+            in.requested_score_mod = c.kind;
+            in.has_scale = c.has_scale;
+            in.scale_value = 0.125f;
+            in.requested_bias_kind = c.has_bias ? of::BiasKind::SameShapeTile : of::BiasKind::None;
+            const of::RuntimePlan plan = of::make_runtime_plan(in, false, false);
+            all_hip = all_hip && plan.qk_backend == of::QkBackendKind::Hip;
+            std::vector<float> expected(tiles * sh.m * sh.n);
+            for (std::size_t t = 0; t < tiles; ++t)
+                for (std::size_t i = 0; i < sh.m; ++i)
+                    for (std::size_t j = 0; j < sh.n; ++j) {
+                        float value = 0.0f;
+                        for (std::size_t kk = 0; kk < sh.d; ++kk)
+                            value += q[(t * sh.m + i) * sh.d + kk] * k[(t * sh.n + j) * sh.d + kk];
+                        if (c.has_scale) value *= 0.125f;
+                        if (c.has_bias) value += bias[(t * sh.m + i) * sh.n + j];
+                        expected[(t * sh.m + i) * sh.n + j] = value;
+                    }
+            const of::StridedMatmulShape st{sh.m, sh.n, sh.d, sh.d, 1, 1, sh.d, sh.n, 1};
+            for (int defer = 0; defer < 2; ++defer) {
+                std::vector<float> actual(expected.size(), 0.0f);
+                of::QkScoreTileExecuteOptions opts;
+                if (defer) opts.sync_mode = of::QkScoreTileSyncMode::DeferUntilExplicitWait;
+                of::QkScoreTileDebugInfo debug;
+                for (std::size_t t = 0; t < tiles; ++t) {
+                    of::QkScoreTilePostOpsInput post;
+                    post.additive_bias = c.has_bias ? bias.data() + t * sh.m * sh.n : nullptr;
+                    post.additive_bias_stride_m = sh.n;
+                    post.additive_bias_stride_n = 1;
+                    of::qk_score_tile_inplace_with_options(q.data() + t * sh.m * sh.d,
+                                                           k.data() + t * sh.n * sh.d,
+                                                           actual.data() + t * sh.m * sh.n, st, plan,
+                                                           post, opts, &debug);
+                }
+                if (defer) of::qk_score_tile_wait_for_onednn();
+                const bool exact = std::memcmp(actual.data(), expected.data(), expected.size() * 4) == 0;
+                all_exact = all_exact && exact && debug.backend == of::QkBackendKind::Hip &&
+                            debug.lowering_status == of::LoweringStatus::LoweredToHipKernel;
+                if (!exact)
+                    std::printf("  qk_score_tile %dx%dx%zux%zux%zu %s defer=%d: max diff %g\n", sh.batch,
+                                sh.heads, sh.m, sh.n, sh.d, c.name, defer, of::max_abs_diff(actual, expected));
+            }
+        }
+    }
+    expect(all_hip, "make_runtime_plan picks the HIP backend", all_hip ? 1.0 : 0.0);
+    expect(all_exact, "qk_score_tile_inplace: 18 records bit-exact", all_exact ? 1.0 : 0.0);
+
+    // cache and wait counters
+    of::qk_score_tile_reset_cache_stats();
+    std::vector<float> q(64 * 32, 0.5f), k(64 * 32, 0.25f), s(64 * 64);
+    of::RuntimePlanInput in;
+    in.query_length = in.key_length = 64;
+    in.head_dim = in.value_dim = 32;
+    const of::RuntimePlan plan = of::make_runtime_plan(in, false, false);
+    const of::StridedMatmulShape st{64, 64, 32, 32, 1, 1, 32, 64, 1};
+    for (int i = 0; i < 3; ++i) of::qk_score_tile_inplace(q.data(), k.data(), s.data(), st, plan, {});
+    of::QkScoreTileExecuteOptions deferred;
+    deferred.sync_mode = of::QkScoreTileSyncMode::DeferUntilExplicitWait;
+    of::qk_score_tile_inplace_with_options(q.data(), k.data(), s.data(), st, plan, {}, deferred);
+    of::qk_score_tile_wait_for_onednn();
+    const auto stats = of::qk_score_tile_get_cache_stats();
+    expect(stats.immediate_waits == 3 && stats.deferred_waits == 1 && stats.cache_size == 1 &&
+               stats.primitive_cache_hits + stats.primitive_cache_misses == 4,
+           "qk_score_tile cache stats", static_cast<double>(stats.primitive_cache_hits));
+    expect(s[0] == 4.0f, "qk_score_tile value 32*0.5*0.25", s[0]);
+
+    // error contract (qk_score_tile.cpp:16-26,36-47)
+    expect_throw<std::invalid_argument>([&] {
+        of::qk_score_tile_inplace(q.data(), k.data(), s.data(), of::StridedMatmulShape{0, 64, 32, 32, 1, 1, 32, 64, 1},
+                                  plan, {});
+    }, "qk_score_tile zero dims throws invalid_argument");
+    expect_throw<std::invalid_argument>([&] {
+        of::qk_score_tile_inplace(nullptr, k.data(), s.data(), st, plan, {});
+    }, "qk_score_tile null pointer throws invalid_argument");
+    expect_throw<std::invalid_argument>([&] {
+        of::RuntimePlanInput bin = in;
+        bin.requested_score_mod = of::ScoreModKind::AdditiveBias;
+        bin.requested_bias_kind = of::BiasKind::SameShapeTile;
+        of::qk_score_tile_inplace(q.data(), k.data(), s.data(), st, of::make_runtime_plan(bin, false, false), {});
+    }, "qk_score_tile missing bias throws invalid_argument");
 }
 
 int main() {
@@ -112,21 +222,25 @@ int main() {
     for (int i = 0; i < 15; ++i) a[i] = 0.5f * i - 3.0f;
     for (int i = 0; i < 21; ++i) b[i] = 0.25f * i - 2.0f;
     const auto c = of::matmul_tile(of::TileKernelKind::HipMfma, a, b, ms);
-    double gemm_err = 0.0;
+    std::vector<float> c_ref(35);
     for (int i = 0; i < 5; ++i)
         for (int j = 0; j < 7; ++j) {
-            double s = 0.0;
+            float s = 0.0f;
             for (int kk = 0; kk < 3; ++kk) s += a[i * 3 + kk] * b[kk * 7 + j];
-            gemm_err = std::max(gemm_err, std::fabs(s - c[i * 7 + j]));
+            c_ref[i * 7 + j] = s;
         }
-    expect(gemm_err <= 1e-5, "matmul_tile", gemm_err);
+    expect(std::memcmp(c.data(), c_ref.data(), 35 * 4) == 0, "matmul_tile (bit-exact)",
+           of::max_abs_diff(c, c_ref));
     std::vector<float> kt(7 * 3);  // K[7,3] row-major, read as B = K^T [3,7]
     for (int j = 0; j < 7; ++j)
         for (int kk = 0; kk < 3; ++kk) kt[j * 3 + kk] = b[kk * 7 + j];
     std::vector<float> cs(35, 0.0f);
     of::matmul_tile_strided_inplace(of::TileKernelKind::Reference, a.data(), kt.data(), cs.data(),
                                     of::StridedMatmulShape{5, 7, 3, 3, 1, 1, 3, 7, 1});
-    expect(of::max_abs_diff(cs, c) <= 1e-6f, "matmul_tile_strided_inplace", of::max_abs_diff(cs, c));
+    expect(std::memcmp(cs.data(), c.data(), 35 * 4) == 0, "matmul_tile_strided_inplace (bit-exact)",
+           of::max_abs_diff(cs, c));
+
+    qk_score_checks();
 
     // error contract
     expect_throw<std::invalid_argument>([&] { of::standard_attention(q, k, std::vector<float>(3), shape, options); },

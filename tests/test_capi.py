@@ -48,7 +48,16 @@ def test_cpp_api_symbols_exported(ofh):
                 "onednn_flash::BlockMask::allows(", "onednn_flash::matmul_tile(",
                 "onednn_flash::matmul_tile_inplace(", "onednn_flash::matmul_tile_strided_inplace(",
                 "onednn_flash::matmul_tile_reference(", "onednn_flash::matmul_tile_reference_inplace(",
-                "onednn_flash::tile_kernel_name(", "onednn_flash::AttentionWorkspace::resize("):
+                "onednn_flash::tile_kernel_name(", "onednn_flash::AttentionWorkspace::resize(",
+                "onednn_flash::make_score_mod_plan(", "onednn_flash::make_hip_score_mod_plan(",
+                "onednn_flash::make_runtime_plan(", "onednn_flash::make_runtime_plan_cache_key(",
+                "onednn_flash::make_block_mask_plan(",
+                "onednn_flash::make_causal_mask_tile_descriptor(",
+                "onednn_flash::hip_backend_available(", "onednn_flash::qk_score_tile_inplace(",
+                "onednn_flash::qk_score_tile_inplace_with_options(",
+                "onednn_flash::qk_score_tile_wait_for_onednn(",
+                "onednn_flash::qk_score_tile_get_cache_stats(",
+                "onednn_flash::qk_score_tile_reset_cache_stats("):
         assert sym in out, sym
 
 
@@ -58,6 +67,59 @@ def test_struct_layout_matches(ofh):
     assert p.struct_size == ctypes.sizeof(ofh.AttentionParams)
     assert p.scale == 1.0 and p.dtype == ofh.DTYPE_F32 and p.algorithm == ofh.ALGO_AUTO
     assert ofh.lib().ofh_abi_version() == 1
+
+
+def test_qk_score_struct_layout(ofh):
+    p = ofh.QkScoreParams()
+    ofh.lib().ofh_qk_score_params_init(ctypes.byref(p))
+    assert p.struct_size == ctypes.sizeof(ofh.QkScoreParams)
+    assert (p.batch, p.dtype, p.has_scale, p.scale, p.algorithm) == (1, ofh.DTYPE_F32, 0, 1.0,
+                                                                   ofh.QK_AUTO)
+    assert p.bias is None and p.softcap == 0.0
+
+
+def _qk_params(ofh, m=4, n=4, k=8, **kw):
+    p = ofh.QkScoreParams()
+    ofh.lib().ofh_qk_score_params_init(ctypes.byref(p))
+    p.m, p.n, p.k = m, n, k
+    p.a_stride_m, p.a_stride_k, p.b_stride_k, p.b_stride_n, p.c_stride_m, p.c_stride_n = k, 1, 1, k, n, 1
+    for name, value in kw.items():
+        setattr(p, name, value)
+    return p
+
+
+def test_qk_score_validation_messages(ofh):
+    """The reference's messages (qk_score_tile.cpp:16-26); every case fails on
+    the host before any device work, so fake non-null addresses are safe."""
+    F = ofh
+
+    def err(p, q=16, k=32, c=48):
+        rc = F.lib().ofh_qk_score_tile(ctypes.byref(p), q, k, c, None)
+        return rc, F.lib().ofh_last_error().decode()
+
+    assert err(_qk_params(F, m=0)) == (F.OFH_ERROR_INVALID_ARGUMENT,
+                                       "QK score tile dimensions must be non-zero")
+    assert err(_qk_params(F, k=0)) == (F.OFH_ERROR_INVALID_ARGUMENT,
+                                       "QK score tile dimensions must be non-zero")
+    assert err(_qk_params(F), q=None) == (F.OFH_ERROR_INVALID_ARGUMENT,
+                                          "QK score tile pointers must be non-null")
+    assert err(_qk_params(F), c=None)[1] == "QK score tile pointers must be non-null"
+    assert "batch" in err(_qk_params(F, batch=0))[1]
+    assert "non-negative" in err(_qk_params(F, a_stride_m=-1))[1]
+    assert err(_qk_params(F, dtype=9))[1] == "unknown dtype"
+    assert "softcap" in err(_qk_params(F, softcap=-2.0))[1]
+    assert err(_qk_params(F, algorithm=5))[1] == "unknown algorithm"
+    rc, msg = err(_qk_params(F, algorithm=F.QK_MFMA))                  # fp32
+    assert rc == F.OFH_ERROR_UNSUPPORTED and "MFMA QK score tile needs" in msg
+    rc, msg = err(_qk_params(F, algorithm=F.QK_MFMA, dtype=F.DTYPE_BF16, k=12, a_stride_m=12,
+                             b_stride_n=12))                            # k % 8 != 0
+    assert rc == F.OFH_ERROR_UNSUPPORTED
+    rc, msg = err(_qk_params(F, algorithm=F.QK_MFMA, dtype=F.DTYPE_BF16), q=18)  # misaligned
+    assert rc == F.OFH_ERROR_UNSUPPORTED
+    p = _qk_params(F)
+    p.struct_size = 8
+    assert "struct_size" in err(p)[1]
+    assert err(_qk_params(F, m=65535 * 32 + 1))[1] == "QK score tile exceeds the grid range"
 
 
 def _expect_error(ofh, p, code, text):
