@@ -15,6 +15,8 @@
 //                     (matrix-core kernel; checked against the fp32 upcast)
 //   cpu_loop          the checking loop itself, the reference's CPU reference
 //                     path (shapes up to 128 x 128 only)
+// Shapes: the reference's three; --large adds 32 heads of 1024^2 and of
+// 4096^2 with d = 128 (device-resident backends only); --large-only runs just those.
 // time_ms* are wall-clock per batch (as the reference); device_time_ms_* come
 // from HIP events around the device-resident calls.
 
@@ -449,7 +451,7 @@ int main(int argc, char** argv) {
     std::string json_path = "gpurun_out/qk_postops/cpp-qk-postops.json";
     std::string csv_path = "gpurun_out/qk_postops/cpp-qk-postops.csv";
     int warmup = 2, repeat = 5;
-    bool include_deferred = false, large = false;
+    bool include_deferred = false, large = false, large_only = false;
     for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
         if (a == "--output-json" && i + 1 < argc) json_path = argv[++i];
@@ -458,6 +460,7 @@ int main(int argc, char** argv) {
         else if (a == "--repeat" && i + 1 < argc) repeat = std::stoi(argv[++i]);
         else if (a == "--include-deferred-wait") include_deferred = true;
         else if (a == "--large") large = true;
+        else if (a == "--large-only") large = large_only = true;
         else {
             std::cerr << "Unknown argument: " << a << "\n";
             return 2;
@@ -473,6 +476,7 @@ int main(int argc, char** argv) {
         hipDeviceProp_t prop;
         hip_ok(hipGetDeviceProperties(&prop, dev), "hipGetDeviceProperties");
         std::vector<ShapeCase> shapes{{1, 1, 64, 64, 32, 32}, {1, 1, 128, 128, 64, 64}, {1, 4, 128, 128, 64, 64}};
+        if (large_only) shapes.clear();
         const std::size_t reference_shapes = shapes.size();
         if (large) {
             shapes.push_back({1, 32, 1024, 1024, 128, 128});

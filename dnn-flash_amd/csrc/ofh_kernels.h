@@ -91,6 +91,7 @@ struct QkScoreArgs {
     const float* bias;
     int64_t bias_sm, bias_sn, bias_sb;
     float softcap;
+    int vec4;   // set by the launcher: 16-byte score (and bias) row runs are aligned
 };
 
 // Launchers; each returns the hipError_t of the launch.

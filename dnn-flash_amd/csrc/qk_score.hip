@@ -109,12 +109,14 @@ struct QkMfma<_Float16> {
 
 // 128x128 score block per workgroup, 4 wavefronts of 64x64 (2x2 MFMA tiles of
 // 32x32). Operand lane layout of the 32x32x16 MFMA: lane l holds row (l & 31)
-// of Q (A) and row (l & 31) of K (B = K^T column), k elements 8*(l >> 5) .. +7
-// of the 16-wide step. Output element e of lane l is row 8*(e >> 2) +
-// 4*(l >> 5) + (e & 3), column l & 31 of the 32x32 tile.
+// of the A operand and column (l & 31) of the B operand, k elements
+// 8*(l >> 5) .. +7 of the 16-wide step; output element e of lane l is row
+// 8*(e >> 2) + 4*(l >> 5) + (e & 3), column l & 31. With A = K and B = Q^T
+// the tile is S^T, so each lane owns runs of 4 consecutive keys of one query
+// row: contiguous in the row-major score matrix.
 constexpr int kMfmaBlock = 128;
 
-template <typename T>
+template <typename T, bool CAP>
 __global__ __launch_bounds__(256) void qk_score_mfma_kernel(QkScoreArgs a) {
     // Scale and bias are rounded separately, as the reference applies them.
 #pragma clang fp contract(off)
@@ -157,24 +159,49 @@ __global__ __launch_bounds__(256) void qk_score_mfma_kernel(QkScoreArgs a) {
 #pragma unroll
         for (int x = 0; x < 2; ++x)
 #pragma unroll
-            for (int y = 0; y < 2; ++y) acc[x][y] = QkMfma<T>::run(qa[x], kb[y], acc[x][y]);
+            for (int y = 0; y < 2; ++y) acc[x][y] = QkMfma<T>::run(kb[y], qa[x], acc[x][y]);
     }
+    // acc[x][y] holds the transposed tile: lane column r is query i0+32x+r and
+    // elements 4g..4g+3 are the four consecutive keys j0+32y+8g+4*half+0..3,
+    // written with one 16-byte store where the layout allows it.
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
+        const int64_t i = i0 + 32 * x + r;
+        if (i >= a.M) continue;
+        float* crow = a.c + bt * a.c_sb + i * a.c_sm;
+        const float* brow = a.bias != nullptr ? a.bias + bt * a.bias_sb + i * a.bias_sm : nullptr;
 #pragma unroll
         for (int y = 0; y < 2; ++y) {
-            const int64_t j = j0 + 32 * y + r;
-            if (j >= a.N) continue;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int64_t i = i0 + 32 * x + 8 * (e >> 2) + 4 * half + (e & 3);
-                if (i >= a.M) continue;
-                float v = acc[x][y][e];
-                if (a.has_scale) v = v * a.scale;
-                if (a.bias != nullptr)
-                    v = v + a.bias[bt * a.bias_sb + i * a.bias_sm + j * a.bias_sn];
-                if (a.softcap > 0.0f) v = a.softcap * tanhf(v / a.softcap);
-                a.c[bt * a.c_sb + i * a.c_sm + j * a.c_sn] = v;
+            for (int g = 0; g < 4; ++g) {
+                const int64_t jb = j0 + 32 * y + 8 * g + 4 * half;
+                if (jb >= a.N) continue;
+                float v[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v[u] = a.has_scale ? acc[x][y][4 * g + u] * a.scale : acc[x][y][4 * g + u];
+                if (a.vec4 && jb + 3 < a.N) {
+                    if (brow != nullptr) {
+                        const float4 b4 = *(const float4*)(brow + jb);
+                        v[0] = v[0] + b4.x;
+                        v[1] = v[1] + b4.y;
+                        v[2] = v[2] + b4.z;
+                        v[3] = v[3] + b4.w;
+                    }
+                    if (CAP)
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) v[u] = a.softcap * tanhf(v[u] / a.softcap);
+                    *(float4*)(crow + jb) = make_float4(v[0], v[1], v[2], v[3]);
+                } else {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int64_t j = jb + u;
+                        if (j >= a.N) break;
+                        float w = v[u];
+                        if (brow != nullptr) w = w + brow[j * a.bias_sn];
+                        if (CAP) w = a.softcap * tanhf(w / a.softcap);
+                        crow[j * a.c_sn] = w;
+                    }
+                }
             }
         }
     }
@@ -192,8 +219,13 @@ bool qk_score_mfma_supported(const QkScoreArgs& a, int dtype) {
 hipError_t launch_qk_score_mfma(const QkScoreArgs& a, int dtype, hipStream_t s) {
     if (a.batch <= 0 || a.M <= 0 || a.N <= 0 || a.K <= 0) return hipSuccess;
     if (!qk_score_mfma_supported(a, dtype)) return hipErrorInvalidValue;
+    const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    const bool c_vec = a.c_sn == 1 && a.c_sm % 4 == 0 && a.c_sb % 4 == 0 && al16(a.c);
+    const bool b_vec = a.bias == nullptr ||
+                       (a.bias_sn == 1 && a.bias_sm % 4 == 0 && a.bias_sb % 4 == 0 && al16(a.bias));
     for (int64_t b0 = 0; b0 < a.batch; b0 += kMaxGridZ) {
         QkScoreArgs x = a;
+        x.vec4 = c_vec && b_vec;
         x.batch = std::min<int64_t>(kMaxGridZ, a.batch - b0);
         x.q = (const char*)a.q + b0 * a.a_sb * 2;
         x.k = (const char*)a.k + b0 * a.b_sb * 2;
@@ -201,10 +233,16 @@ hipError_t launch_qk_score_mfma(const QkScoreArgs& a, int dtype, hipStream_t s) 
         if (a.bias != nullptr) x.bias = a.bias + b0 * a.bias_sb;
         const dim3 grid((unsigned)((a.N + kMfmaBlock - 1) / kMfmaBlock),
                         (unsigned)((a.M + kMfmaBlock - 1) / kMfmaBlock), (unsigned)x.batch);
-        if (dtype == DT_BF16)
-            hipLaunchKernelGGL(qk_score_mfma_kernel<__bf16>, grid, dim3(256), 0, s, x);
-        else
-            hipLaunchKernelGGL(qk_score_mfma_kernel<_Float16>, grid, dim3(256), 0, s, x);
+        // The soft-cap epilogue is a separate instantiation: it needs many more
+        // registers, which would lower the occupancy of the common case.
+        const bool cap = a.softcap > 0.0f;
+        if (dtype == DT_BF16) {
+            if (cap) hipLaunchKernelGGL((qk_score_mfma_kernel<__bf16, true>), grid, dim3(256), 0, s, x);
+            else hipLaunchKernelGGL((qk_score_mfma_kernel<__bf16, false>), grid, dim3(256), 0, s, x);
+        } else {
+            if (cap) hipLaunchKernelGGL((qk_score_mfma_kernel<_Float16, true>), grid, dim3(256), 0, s, x);
+            else hipLaunchKernelGGL((qk_score_mfma_kernel<_Float16, false>), grid, dim3(256), 0, s, x);
+        }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
