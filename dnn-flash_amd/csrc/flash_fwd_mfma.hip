@@ -232,6 +232,7 @@ __device__ __forceinline__ float online_softmax_tile(const FwdArgs& a, f32x16 (&
 
 constexpr int kBlockN16 = 64;
 constexpr float kRescaleSlack = 8.0f;
+constexpr int kFragAhead = 4;  // LDS fragment reads in flight ahead of the MFMAs (plain scale)
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef short i16x8 __attribute__((ext_vector_type(8)));
@@ -444,14 +445,25 @@ struct Wave32 {
                 for (int sb = 0; sb < BN / 32; ++sb) s[sb] = M16::mma(kf[sb][c], qf[c], s[sb]);
             return;
         }
+        // Fragments are read kFragAhead MFMAs ahead of their use; the
+        // scheduling fences keep the compiler from sinking each read next to
+        // its MFMA (it otherwise keeps two in flight).
+        constexpr int NF = (BN / 32) * (D / 16);
+        auto rd = [&](int i) {
+            const int sb = i / (D / 16), c = i % (D / 16);
+            return __builtin_bit_cast(v8, *(const lds_u32x4*)(kb + 32 * sb * L::KSTR + 32 * c));
+        };
+        v8 f[kFragAhead];
 #pragma unroll
-        for (int sb = 0; sb < BN / 32; ++sb) {
-            s[sb] = f32x16{};
+        for (int i = 0; i < kFragAhead; ++i) f[i] = rd(i);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int c = 0; c < D / 16; ++c) {
-                const v8 af = __builtin_bit_cast(v8, *(const lds_u32x4*)(kb + 32 * sb * L::KSTR + 32 * c));
-                s[sb] = M16::mma(af, qf[c], s[sb]);
-            }
+        for (int sb = 0; sb < BN / 32; ++sb) s[sb] = f32x16{};
+#pragma unroll
+        for (int i = 0; i < NF; ++i) {
+            s[i / (D / 16)] = M16::mma(f[i % kFragAhead], qf[i % (D / 16)], s[i / (D / 16)]);
+            if (i + kFragAhead < NF) f[i % kFragAhead] = rd(i + kFragAhead);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 
@@ -479,10 +491,19 @@ struct Wave32 {
                 for (int db = 0; db < D / 32; ++db) o[db] = M16::mma(vf[db][c], pf[c], o[db]);
             return;
         }
+        // V^T fragments kFragAhead MFMAs ahead (see qk)
+        constexpr int NF = (D / 32) * (BN / 16);
+        v8 f[kFragAhead];
 #pragma unroll
-        for (int db = 0; db < D / 32; ++db)
+        for (int i = 0; i < kFragAhead; ++i) f[i] = vfrag(i % (BN / 16), i / (BN / 16));
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int c = 0; c < BN / 16; ++c) o[db] = M16::mma(vfrag(c, db), pf[c], o[db]);
+        for (int i = 0; i < NF; ++i) {
+            o[i / (BN / 16)] = M16::mma(f[i % kFragAhead], pf[i % (BN / 16)], o[i / (BN / 16)]);
+            if (i + kFragAhead < NF)
+                f[i % kFragAhead] = vfrag((i + kFragAhead) % (BN / 16), (i + kFragAhead) / (BN / 16));
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
 
     // Scores in log2 units with the call's score_mod: scale, then ALiBi
@@ -737,9 +758,17 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
     for (int it = 0; it < ntiles; ++it) {
         const int stage = (it & 1) * L::STAGE;
         if (w.tile_active(e_cur)) {
+            // Plain scale: matrix phases at wave priority 1 and the softmax at
+            // 0, so that a wavefront ready for MFMAs issues first when the two
+            // wavefronts of a SIMD drift apart (measured +1-2 %; with a
+            // score_mod the longer softmax is better left at equal priority).
+            if (MOD == MOD_PLAIN) __builtin_amdgcn_s_setprio(1);
             w.qk(stage);
+            if (MOD == MOD_PLAIN) __builtin_amdgcn_s_setprio(0);
             w.softmax(e_cur);
+            if (MOD == MOD_PLAIN) __builtin_amdgcn_s_setprio(1);
             w.pv(stage);
+            if (MOD == MOD_PLAIN) __builtin_amdgcn_s_setprio(0);
         }
         if (it + 1 < ntiles) w.store_tile(((it + 1) & 1) * L::STAGE);
         if (it + 2 < ntiles) w.load_tile(w.tile_of(e_nn));
