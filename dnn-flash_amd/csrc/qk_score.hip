@@ -116,29 +116,80 @@ struct QkMfma<_Float16> {
 // row: contiguous in the row-major score matrix.
 constexpr int kMfmaBlock = 128;
 
+// LDS of the matrix-core score kernel, 32 KB so that three workgroups fit a CU
+// (their registers allow three). Unpadded rows (the DMA copies below write
+// consecutive bytes) with XOR-swizzled 16-byte chunks, chosen so that every
+// access pattern below touches 16 distinct bank groups per 16 lanes.
+//
+// Operands: per 64-wide k chunk, the workgroup's 128 Q rows and 128 K rows,
+// 128 bytes each, copied global -> LDS by global_load_lds_dwordx4 (a
+// wavefront writes 1 KB of consecutive LDS: eight rows). Chunk c of row r sits
+// at position c ^ ((r >> 1) & 7): a fragment read takes 16 consecutive rows at
+// one chunk, and rows r, r + 1 share a 256-byte bank line.
+//
+// Epilogue: each wavefront's 64x64 fp32 block in two passes of 32 rows x 256
+// bytes, chunk c of row r at c ^ (r & 15); written 16 rows x one chunk per 16
+// lanes, read back one row (16 chunks) per 16 lanes.
+constexpr int kChunkK = 64;
+constexpr int kRowBytes = kChunkK * 2;
+constexpr int kOperandBytes = 2 * kMfmaBlock * kRowBytes;  // Q then K: 32 KB
+constexpr int kStageBytes = 4 * 32 * 256;                  // 32 rows x 64 fp32 per wavefront: 32 KB
+constexpr int kQkLdsBytes = kOperandBytes > kStageBytes ? kOperandBytes : kStageBytes;
+
+typedef __attribute__((address_space(3))) unsigned char qk_lds_u8;
+typedef __attribute__((address_space(3))) qk_u32x4 qk_lds_u32x4;
+
+// One 16-byte global -> LDS copy per lane; `dst` is the wavefront's LDS base
+// (lane L writes dst + 16 L).
+__device__ __forceinline__ void dma16(const void* src, qk_lds_u8* dst) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+}
+__device__ __forceinline__ qk_u32x4 lds_read16(const qk_lds_u8* p) { return *(const qk_lds_u32x4*)p; }
+typedef float qk_f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) qk_f32x4 qk_lds_f32x4;
+__device__ __forceinline__ void lds_write_f4(qk_lds_u8* p, qk_f32x4 v) { *(qk_lds_f32x4*)p = v; }
+__device__ __forceinline__ qk_f32x4 lds_read_f4(const qk_lds_u8* p) { return *(const qk_lds_f32x4*)p; }
+
 template <typename T, bool CAP>
 __global__ __launch_bounds__(256) void qk_score_mfma_kernel(QkScoreArgs a) {
     // Scale and bias are rounded separately, as the reference applies them.
 #pragma clang fp contract(off)
+    __shared__ __attribute__((aligned(16))) unsigned char smem[kQkLdsBytes];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t bt = blockIdx.z;
-    const int64_t i0 = (int64_t)blockIdx.y * kMfmaBlock + (wave >> 1) * 64;
-    const int64_t j0 = (int64_t)blockIdx.x * kMfmaBlock + (wave & 1) * 64;
+    const int64_t qb0 = (int64_t)blockIdx.y * kMfmaBlock, kb0 = (int64_t)blockIdx.x * kMfmaBlock;
+    const int64_t i0 = qb0 + (wave >> 1) * 64;
+    const int64_t j0 = kb0 + (wave & 1) * 64;
     const T* q = (const T*)a.q + bt * a.a_sb;
     const T* k = (const T*)a.k + bt * a.b_sb;
     const int r = lane & 31, half = lane >> 5;
-    // Row pointers (clamped to row 0 when out of range; such lanes load zeros).
-    const T* qrow[2];
-    const T* krow[2];
-    bool qok[2], kok[2];
+    qk_lds_u8* lds = (qk_lds_u8*)smem;
+    // DMA copy of one k-chunk: wavefront w, step u copies rows 32u + 8w .. +7
+    // of Q and of K; lane L writes row 32u + 8w + (L >> 3), position L & 7,
+    // holding global chunk (L & 7) ^ ((row >> 1) & 7). Rows past M or N and
+    // chunks past K read clamped in-range addresses; their values are never used.
+    auto copy_chunk = [&](int64_t k0) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int row = 32 * u + 8 * wave + (lane >> 3);
+            const int c = (lane & 7) ^ ((row >> 1) & 7);
+            const int64_t kc = (k0 + 8 * c < a.K) ? k0 + 8 * c : k0;
+            const int64_t qi = min(qb0 + row, a.M - 1), kj = min(kb0 + row, a.N - 1);
+            const int base = (32 * u + 8 * wave) * kRowBytes;
+            dma16(q + qi * a.a_sm + kc, lds + base);
+            dma16(k + kj * a.b_sn + kc, lds + kMfmaBlock * kRowBytes + base);
+        }
+    };
+    // Fragment rows of this lane: Q (B operand) rows and K (A operand) rows.
+    int qoff[2], koff[2], qsw[2], ksw[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-        const int64_t qi = i0 + 32 * t + r, kj = j0 + 32 * t + r;
-        qok[t] = qi < a.M;
-        kok[t] = kj < a.N;
-        qrow[t] = q + (qok[t] ? qi : 0) * a.a_sm + 8 * half;
-        krow[t] = k + (kok[t] ? kj : 0) * a.b_sn + 8 * half;
+        const int qr = (wave >> 1) * 64 + 32 * t + r, kr = (wave & 1) * 64 + 32 * t + r;
+        qoff[t] = qr * kRowBytes;
+        koff[t] = kMfmaBlock * kRowBytes + kr * kRowBytes;
+        qsw[t] = (qr >> 1) & 7;
+        ksw[t] = (kr >> 1) & 7;
     }
     qk_f32x16 acc[2][2];
 #pragma unroll
@@ -148,62 +199,83 @@ __global__ __launch_bounds__(256) void qk_score_mfma_kernel(QkScoreArgs a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[x][y][e] = 0.0f;
     const qk_u32x4 zero = {0u, 0u, 0u, 0u};
-    for (int64_t k0 = 0; k0 < a.K; k0 += 16) {
-        const bool kin = k0 + 8 * half < a.K;   // K is a multiple of 8
-        qk_u32x4 qa[2], kb[2];
+    for (int64_t k0 = 0; k0 < a.K; k0 += kChunkK) {
+        copy_chunk(k0);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wavefront's copies have landed
+        __syncthreads();                      // ... and every other wavefront's
+        const int steps = ((int)min((int64_t)kChunkK, a.K - k0) + 15) / 16;  // 16-wide k steps
+        for (int st = 0; st < steps; ++st) {
+            const int c = 2 * st + half;                     // 16-byte chunk of this lane
+            const bool kin = k0 + 8 * c < a.K;               // K is a multiple of 8
+            qk_u32x4 qa[2], kb[2];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            qa[t] = (qok[t] && kin) ? *(const qk_u32x4*)(qrow[t] + k0) : zero;
-            kb[t] = (kok[t] && kin) ? *(const qk_u32x4*)(krow[t] + k0) : zero;
+            for (int t = 0; t < 2; ++t) {
+                qa[t] = kin ? lds_read16(lds + qoff[t] + 16 * (c ^ qsw[t])) : zero;
+                kb[t] = kin ? lds_read16(lds + koff[t] + 16 * (c ^ ksw[t])) : zero;
+            }
+#pragma unroll
+            for (int x = 0; x < 2; ++x)
+#pragma unroll
+                for (int y = 0; y < 2; ++y) acc[x][y] = QkMfma<T>::run(kb[y], qa[x], acc[x][y]);
         }
-#pragma unroll
-        for (int x = 0; x < 2; ++x)
-#pragma unroll
-            for (int y = 0; y < 2; ++y) acc[x][y] = QkMfma<T>::run(kb[y], qa[x], acc[x][y]);
+        __syncthreads();  // the next chunk (or the epilogue) overwrites the operands
     }
     // acc[x][y] holds the transposed tile: lane column r is query i0+32x+r and
-    // elements 4g..4g+3 are the four consecutive keys j0+32y+8g+4*half+0..3,
-    // written with one 16-byte store where the layout allows it.
+    // elements 4g..4g+3 are the four consecutive keys j0+32y+8g+4*half+0..3.
+    // The block goes through LDS (two passes of 32 rows) so that the global
+    // stores and bias loads are full 256-byte row segments: 16 lanes per row,
+    // four rows per instruction.
+    qk_lds_u8* st = lds + wave * 32 * 256;  // this wavefront's 32-row pass buffer
+    const int col = 4 * (lane & 15);
+    const int64_t jb = j0 + col;
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
-        const int64_t i = i0 + 32 * x + r;
-        if (i >= a.M) continue;
-        float* crow = a.c + bt * a.c_sb + i * a.c_sm;
-        const float* brow = a.bias != nullptr ? a.bias + bt * a.bias_sb + i * a.bias_sm : nullptr;
+        // pass x: rows 32x .. 32x+31 of the wavefront's block
 #pragma unroll
-        for (int y = 0; y < 2; ++y) {
+        for (int y = 0; y < 2; ++y)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const int64_t jb = j0 + 32 * y + 8 * g + 4 * half;
-                if (jb >= a.N) continue;
-                float v[4];
+                const int chunk = 8 * y + 2 * g + half;  // keys 32y + 8g + 4 half .. +3
+                lds_write_f4(st + r * 256 + 16 * (chunk ^ (r & 15)),
+                             qk_f32x4{acc[x][y][4 * g], acc[x][y][4 * g + 1], acc[x][y][4 * g + 2], acc[x][y][4 * g + 3]});
+            }
+        __syncthreads();
+#pragma unroll 4
+        for (int it = 0; it < 8; ++it) {
+            const int row = 4 * it + (lane >> 4);
+            const int64_t i = i0 + 32 * x + row;
+            if (i >= a.M || jb >= a.N) continue;
+            const qk_f32x4 raw = lds_read_f4(st + row * 256 + 16 * ((lane & 15) ^ (row & 15)));
+            float v[4] = {raw[0], raw[1], raw[2], raw[3]};
 #pragma unroll
-                for (int u = 0; u < 4; ++u) v[u] = a.has_scale ? acc[x][y][4 * g + u] * a.scale : acc[x][y][4 * g + u];
-                if (a.vec4 && jb + 3 < a.N) {
-                    if (brow != nullptr) {
-                        const float4 b4 = *(const float4*)(brow + jb);
-                        v[0] = v[0] + b4.x;
-                        v[1] = v[1] + b4.y;
-                        v[2] = v[2] + b4.z;
-                        v[3] = v[3] + b4.w;
-                    }
-                    if (CAP)
+            for (int u = 0; u < 4; ++u) v[u] = a.has_scale ? v[u] * a.scale : v[u];
+            float* crow = a.c + bt * a.c_sb + i * a.c_sm;
+            const float* brow = a.bias != nullptr ? a.bias + bt * a.bias_sb + i * a.bias_sm : nullptr;
+            if (a.vec4 && jb + 3 < a.N) {
+                if (brow != nullptr) {
+                    const float4 b4 = *(const float4*)(brow + jb);
+                    v[0] = v[0] + b4.x;
+                    v[1] = v[1] + b4.y;
+                    v[2] = v[2] + b4.z;
+                    v[3] = v[3] + b4.w;
+                }
+                if (CAP)
 #pragma unroll
-                        for (int u = 0; u < 4; ++u) v[u] = a.softcap * tanhf(v[u] / a.softcap);
-                    *(float4*)(crow + jb) = make_float4(v[0], v[1], v[2], v[3]);
-                } else {
+                    for (int u = 0; u < 4; ++u) v[u] = a.softcap * tanhf(v[u] / a.softcap);
+                *(float4*)(crow + jb) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        const int64_t j = jb + u;
-                        if (j >= a.N) break;
-                        float w = v[u];
-                        if (brow != nullptr) w = w + brow[j * a.bias_sn];
-                        if (CAP) w = a.softcap * tanhf(w / a.softcap);
-                        crow[j * a.c_sn] = w;
-                    }
+                for (int u = 0; u < 4; ++u) {
+                    const int64_t j = jb + u;
+                    if (j >= a.N) break;
+                    float w = v[u];
+                    if (brow != nullptr) w = w + brow[j * a.bias_sn];
+                    if (CAP) w = a.softcap * tanhf(w / a.softcap);
+                    crow[j * a.c_sn] = w;
                 }
             }
         }
+        __syncthreads();  // the next pass reuses the buffer
     }
 }
 
