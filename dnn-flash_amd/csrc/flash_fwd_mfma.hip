@@ -214,15 +214,11 @@ __device__ __forceinline__ float online_softmax_tile(const FwdArgs& a, f32x16 (&
 // transposed in a separate pass) are free of bank conflicts, with every
 // per-read offset a compile-time immediate.
 //
-// Two workgroup schedules share this tile code:
-//  * ping-pong (plain scale, no block mask): 8 wavefronts in two groups of 4.
-//    While group 0 runs its matrix phase (O += P_{i-1} V_{i-1}; S_i = K_i Q^T)
-//    group 1 runs its softmax phase on the same SIMDs, and the roles swap at
-//    every barrier. Three LDS stages.
-//  * lockstep (score_mod, block-mask lists): all wavefronts run S, softmax
-//    and PV of a tile between two barriers; double-buffered LDS. With a
-//    block-mask list the workgroup has 4 wavefronts (128 query rows), which
-//    wastes fewer partial tiles on fine masks.
+// Workgroup schedule (every 16-bit call): lockstep. All wavefronts run S,
+// softmax and PV of a tile between two barriers; double-buffered LDS.
+// Without a block-mask list the workgroup has 8 wavefronts (256 query rows);
+// with one it has 4 (128 rows), which wastes fewer partial tiles on fine
+// masks.
 //
 // Online softmax with lazy rescaling: the running max m that probabilities
 // are taken against is raised only when a tile's max exceeds it by more than

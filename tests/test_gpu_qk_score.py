@@ -124,6 +124,25 @@ def test_exact_kernel_order_and_rounding(ofh):
     np.testing.assert_array_equal(_bits(got), _bits(O.qk_score_tile(q, k)))
 
 
+@pytest.mark.parametrize("shape", [(64, 64, 64), (32, 128, 64), (128, 32, 64), (16, 16, 32)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_stage1_ramp_cases(ofh, shape):
+    """The known-answer cases of the reference's tests/cpp/test_stage1_minimal.cpp:
+    ramp inputs, scale 0.125. EXACT is bit-identical to the oracle; the MFMA
+    kernel on the bf16 ramp stays within its summation-order bound."""
+    m, n, d = shape
+    q = (np.arange(m * d, dtype=np.float32) * np.float32(0.1)).reshape(1, m, d)
+    k = ((np.arange(n * d, dtype=np.float32) + np.float32(100)) * np.float32(0.1)).reshape(1, n, d)
+    print(f"stage1 ramp {shape}", flush=True)
+    got = _run(ofh, _dev32(q), _dev32(k), scale=0.125, algorithm=ofh.QK_EXACT).cpu().numpy()
+    np.testing.assert_array_equal(_bits(got), _bits(O.qk_score_tile(q, k, scale=0.125)))
+    tq, uq = to_device(q, "bf16")
+    tk, uk = to_device(k, "bf16")
+    ref = O.qk_score_tile(uq, uk, scale=0.125)
+    got = _run(ofh, tq, tk, scale=0.125, algorithm=ofh.QK_MFMA).cpu().numpy()
+    assert np.all(np.abs(got - ref) <= _mfma_bound(uq, uk, 0.125, ref))
+
+
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("shape", [(1, 64, 64, 32), (4, 128, 128, 64), (3, 37, 300, 72),
                                    (2, 129, 131, 8), (1, 256, 256, 128), (2, 1, 1, 264)],

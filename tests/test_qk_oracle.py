@@ -109,6 +109,41 @@ def test_shared_bias_and_softcap():
     assert np.abs(capped).max() < 2.0
 
 
+# The known-answer cases of the reference's tests/cpp/test_stage1_minimal.cpp:92-152:
+# ramp inputs q[i] = 0.1 i, k[i] = 0.1 (i + 100) over [m, d] and [n, d], scale 0.125.
+STAGE1_SHAPES = [(64, 64, 64), (32, 128, 64), (128, 32, 64), (16, 16, 32)]
+
+
+def stage1_inputs(m, n, d):
+    q = (np.arange(m * d, dtype=np.float32) * np.float32(0.1)).reshape(1, m, d)
+    k = ((np.arange(n * d, dtype=np.float32) + np.float32(100)) * np.float32(0.1)).reshape(1, n, d)
+    return q, k
+
+
+@pytest.mark.parametrize("shape", STAGE1_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_stage1_ramp_within_the_sequential_sum_bound(shape):
+    """A sequential fp32 dot product of length d with rounded products is within
+    gamma_d * sum|q k| (gamma_d = d u / (1 - d u), u = 2^-24) of the exact sum
+    of the same fp32 inputs; the scale 0.125 is a power of two and adds no error.
+    A wrong index (q row against a k column) or a dropped term misses by far more."""
+    m, n, d = shape
+    q, k = stage1_inputs(m, n, d)
+    got = O.qk_score_tile(q, k, scale=0.125)[0].astype(np.float64)
+    q64, k64 = q[0].astype(np.float64), k[0].astype(np.float64)
+    exact = (q64 @ k64.T) * 0.125
+    u = 2.0 ** -24
+    gamma = d * u / (1 - d * u)
+    bound = gamma * (np.abs(q64) @ np.abs(k64).T) * 0.125
+    assert np.all(np.abs(got - exact) <= bound)
+    # the closed form of the ramp: sum_l (i d + l)(j d + l + 100) / 100, within the
+    # input rounding of 0.1 (relative 2^-24 per operand)
+    i = np.arange(m)[:, None].astype(np.float64)
+    j = np.arange(n)[None, :].astype(np.float64)
+    ll = np.arange(d, dtype=np.float64)
+    closed = (d * (i * d) * (j * d + 100) + (i * d + j * d + 100) * ll.sum() + (ll ** 2).sum()) / 100 * 0.125
+    np.testing.assert_allclose(got, closed, rtol=4e-6)
+
+
 def test_rejects_empty_tiles():
     with pytest.raises(ValueError, match="dimensions must be non-zero"):
         O.qk_score_tile(np.zeros((1, 0, 4), np.float32), np.zeros((1, 3, 4), np.float32))
