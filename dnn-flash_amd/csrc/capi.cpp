@@ -43,6 +43,8 @@ struct Resolved {
     int block_m, block_n, threads;
     bool paired;         // causal query tiles run in pairs per workgroup
     int num_q_tiles, num_k_tiles;
+    int key_splits;      // workgroups per query tile, each over a range of K/V tiles
+    int split_tiles;     // K/V tile steps per split
 };
 
 void contiguous_strides(int64_t out[3], const int64_t in[3], size_t H, size_t T, size_t last) {
@@ -119,6 +121,40 @@ int validate(const ofh_attention_params* p, bool check_ptrs, const void* q, cons
     return OFH_SUCCESS;
 }
 
+// Key split of the fp32 kernel (one wavefront per SIMD, 128 query rows per
+// workgroup). A call with fewer query-tile workgroups than two per CU leaves
+// the chip idle, and causal calls are bound by their longest query tile; such
+// calls run the K/V tile steps of each query tile in ranges of split_tiles
+// (at least two) sized so that all ranges together fill about 512 workgroups,
+// then merge the partial rows. Without a mask the tile steps of query tile qt
+// are known on the host; with a block mask the list can only remove steps, so
+// the unmasked count is an upper bound.
+void choose_key_splits(const ofh_attention_params* p, Resolved& r) {
+    r.key_splits = 1;
+    r.split_tiles = 1 << 30;
+    if (p->dtype != OFH_DTYPE_F32 || r.paired) return;
+    constexpr int64_t kTargetWorkgroups = 512;
+    constexpr int kMaxSplits = 64;
+    const int64_t bh = (int64_t)p->batch * p->heads;
+    if (bh * r.num_q_tiles >= kTargetWorkgroups) return;
+    int64_t total = 0;
+    int max_steps = 0;
+    for (int qt = 0; qt < r.num_q_tiles; ++qt) {
+        const int64_t kend = p->causal ? std::min<int64_t>((int64_t)p->key_tokens, (int64_t)(qt + 1) * r.block_m)
+                                       : (int64_t)p->key_tokens;
+        const int steps = (int)((kend + r.block_n - 1) / r.block_n);
+        total += steps;
+        max_steps = std::max(max_steps, steps);
+    }
+    total *= bh;
+    const int per = (int)std::max<int64_t>(2, (total + kTargetWorkgroups - 1) / kTargetWorkgroups);
+    int splits = (max_steps + per - 1) / per;
+    if (splits <= 1) return;
+    splits = std::min(splits, kMaxSplits);
+    r.key_splits = splits;
+    r.split_tiles = (max_steps + splits - 1) / splits;
+}
+
 int resolve(const ofh_attention_params* p, const void* q, const void* k, const void* v,
             const void* out, Resolved& r) {
     contiguous_strides(r.qs, p->q_strides, p->heads, p->query_tokens, p->head_dim);
@@ -155,6 +191,8 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
         r.threads = 256;
         r.num_q_tiles = 0;
         r.num_k_tiles = 0;
+        r.key_splits = 1;
+        r.split_tiles = 1 << 30;
         return OFH_SUCCESS;
     }
     r.algorithm = OFH_ALGO_FLASH_MFMA;
@@ -174,13 +212,25 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
         return set_error(OFH_ERROR_UNSUPPORTED, "block-mask tile list too large");
     if (r.tile_list && (r.block_m > ofh::kQueriesPerWave * ofh::kListSlices || r.num_k_tiles > (1 << 22)))
         return set_error(OFH_ERROR_UNSUPPORTED, "block-mask tile list entry cannot encode this tiling");
+    choose_key_splits(p, r);
     return OFH_SUCCESS;
 }
 
-size_t workspace_bytes_for(const Resolved& r) {
+size_t round256(size_t n) { return (n + 255) & ~size_t(255); }
+
+// Workspace layout: [tile counts][tile entries] (block mask), then
+// [partial O][partial (m, l)] (key split).
+size_t list_bytes(const Resolved& r) {
     if (!r.tile_list) return 0;
-    const size_t counts = ((size_t)r.num_q_tiles * 4 + 255) & ~size_t(255);
-    return counts + (size_t)r.num_q_tiles * (size_t)r.num_k_tiles * 4;
+    return round256((size_t)r.num_q_tiles * 4) + (size_t)r.num_q_tiles * (size_t)r.num_k_tiles * 4;
+}
+size_t partial_rows(const ofh_attention_params* p, const Resolved& r) {
+    return (size_t)r.key_splits * p->batch * p->heads * p->query_tokens;
+}
+size_t workspace_bytes_for(const ofh_attention_params* p, const Resolved& r) {
+    size_t n = list_bytes(r);
+    if (r.key_splits > 1) n = round256(n) + round256(partial_rows(p, r) * p->value_dim * 4) + partial_rows(p, r) * 8;
+    return n;
 }
 
 // Library-owned scratch per device, used when the caller passes no workspace.
@@ -250,6 +300,8 @@ ofh::FwdArgs make_args(const ofh_attention_params* p, const Resolved& r, const v
     a.softcap = p->softcap;
     a.inv_softcap = p->softcap > 0.0f ? 1.0f / p->softcap : 0.0f;
     a.out_f32 = p->out_dtype == OFH_DTYPE_F32 ? 1 : 0;
+    a.num_splits = 1;
+    a.split_tiles = 1 << 30;
     return a;
 }
 
@@ -263,16 +315,18 @@ int fwd_impl(const ofh_attention_params* p, const void* q, const void* k, const 
         OFH_HIP_CHECK(ofh::launch_rowwise(a, p->dtype, stream));
         return OFH_SUCCESS;
     }
-    if (r.tile_list) {
-        const size_t need = workspace_bytes_for(r);
-        void* ws = workspace;
+    const size_t need = workspace_bytes_for(p, r);
+    void* ws = workspace;
+    if (need > 0) {
         if (ws == nullptr) {
             if (int rc = library_scratch(need, &ws)) return rc;
         } else if (workspace_bytes < need) {
             return set_error(OFH_ERROR_WORKSPACE_TOO_SMALL,
                              "workspace too small: need " + std::to_string(need) + " bytes");
         }
-        const size_t counts_bytes = ((size_t)r.num_q_tiles * 4 + 255) & ~size_t(255);
+    }
+    if (r.tile_list) {
+        const size_t counts_bytes = round256((size_t)r.num_q_tiles * 4);
         ofh::TileListArgs t;
         t.M = a.M;
         t.N = a.N;
@@ -292,7 +346,17 @@ int fwd_impl(const ofh_attention_params* p, const void* q, const void* k, const 
         a.tile_counts = t.counts;
         a.tile_entries = t.entries;
     }
+    a.num_splits = r.key_splits;
+    a.split_tiles = r.split_tiles;
+    a.split_bm = r.block_m;
+    a.split_bn = r.block_n;
+    if (r.key_splits > 1) {
+        char* base = static_cast<char*>(ws) + round256(list_bytes(r));
+        a.part_o = reinterpret_cast<float*>(base);
+        a.part_ml = reinterpret_cast<float*>(base + round256(partial_rows(p, r) * p->value_dim * 4));
+    }
     OFH_HIP_CHECK(ofh::launch_flash_mfma(a, p->dtype, r.general_mod, stream));
+    if (r.key_splits > 1) OFH_HIP_CHECK(ofh::launch_combine_splits(a, stream));
     return OFH_SUCCESS;
 }
 
@@ -347,7 +411,7 @@ int ofh_attention_workspace_bytes(const ofh_attention_params* p, size_t* bytes) 
     static const char dummy[16] __attribute__((aligned(16))) = {0};
     Resolved r;
     if (int rc = resolve(p, dummy, dummy, dummy, dummy, r)) return rc;
-    *bytes = workspace_bytes_for(r);
+    *bytes = workspace_bytes_for(p, r);
     return OFH_SUCCESS;
 }
 
@@ -447,13 +511,16 @@ int ofh_attention_launch_info(const ofh_attention_params* p, ofh_launch_info* in
         info->block_m = r.block_m;
         info->block_n = r.block_n;
         info->threads = r.threads;
-        info->workgroups = (int64_t)p->batch * p->heads * (r.paired ? (r.num_q_tiles + 1) / 2 : r.num_q_tiles);
+        info->workgroups = (int64_t)p->batch * p->heads * (r.paired ? (r.num_q_tiles + 1) / 2 : r.num_q_tiles) *
+                           r.key_splits;
+        info->key_splits = r.key_splits;
         name = ofh::flash_mfma_kernel_name(p->dtype, (int)p->head_dim, r.general_mod, r.tile_list);
     } else {
         info->block_m = 1;
         info->block_n = 64;
         info->threads = 256;
         info->workgroups = ((int64_t)p->batch * p->heads * p->query_tokens + 3) / 4;
+        info->key_splits = 1;
         name = "rowwise_fwd_kernel";
     }
     std::strncpy(info->kernel_name, name, sizeof(info->kernel_name) - 1);

@@ -818,7 +818,9 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a)
     const int g = lane >> 5, r = lane & 31;
 
     int bh, qt;
-    map_work(blockIdx.x, a.B * a.H, a.num_q_tiles, a.causal, bh, qt);
+    const int tiles_per_split = a.B * a.H * a.num_q_tiles;
+    const int split = (int)blockIdx.x / tiles_per_split;
+    map_work((int)blockIdx.x - split * tiles_per_split, a.B * a.H, a.num_q_tiles, a.causal, bh, qt);
     const int b = bh / a.H, h = bh - b * a.H;
     const float* __restrict__ Qp = (const float*)a.q + b * a.q_sb + h * a.q_sh;
     const float* __restrict__ Kp = (const float*)a.k + b * a.k_sb + h * a.k_sh;
@@ -848,6 +850,10 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a)
         const int kend = a.causal ? min(a.N, q0 + kBlockM32) : a.N;
         ntiles = (kend + BN - 1) / BN;
     }
+    // tile steps [it0, it1) of this workgroup's key split
+    const int it0 = split * a.split_tiles;
+    const int it1 = min(ntiles, it0 + a.split_tiles);
+    if (a.num_splits > 1 && it0 >= it1) return;  // no key tile in this split (the combine skips it)
 
     f32x4 kreg[CPT], vreg[CPT];
     auto load_tile = [&](int kt) {
@@ -894,22 +900,22 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a)
     if (GENERAL && a.bias_kind == BIAS_DENSE && my_q < a.M)
         bias_row = a.bias + b * a.bias_sb + h * a.bias_sh + (int64_t)my_q * a.bias_sm;
 
-    if (ntiles > 0) {
+    if (it0 < it1) {
         int e0;
-        load_tile(tile_at(0, e0));
+        load_tile(tile_at(it0, e0));
     }
     wait_vm_loads();
-    if (ntiles > 0) store_tile(0);
+    if (it0 < it1) store_tile(0);
     __syncthreads();
 
-    for (int it = 0; it < ntiles; ++it) {
+    for (int it = it0; it < it1; ++it) {
         int ent;
         const int kt = tile_at(it, ent);
-        if (it + 1 < ntiles) {
+        if (it + 1 < it1) {
             int en;
             load_tile(tile_at(it + 1, en));
         }
-        const float* Ks = lds + (it & 1) * STAGE;
+        const float* Ks = lds + ((it - it0) & 1) * STAGE;
         const float* Vs = Ks + KTILE;
         const int k0 = kt * BN;
         const bool active = list != nullptr ? list_any(ent, wave)
@@ -939,11 +945,33 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a)
                     o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * db], s[0][u], o[db], 0, 0, 0);
             }
         }
-        if (it + 1 < ntiles) store_tile((it + 1) & 1);
+        if (it + 1 < it1) store_tile((it + 1 - it0) & 1);
         __syncthreads();
     }
 
     const float l_tot = l_run + __shfl_xor(l_run, 32);
+    if (a.num_splits > 1) {
+        // partial row: unnormalised O and (m, l); the combine merges the splits
+        if (my_q < a.M) {
+            const int64_t prow = ((int64_t)split * a.B * a.H + bh) * a.M + my_q;
+            float* po = a.part_o + prow * D + 4 * g;
+#pragma unroll
+            for (int db = 0; db < D / 32; ++db) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    f32x4 val;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) val[j] = o[db][4 * i + j];
+                    *(f32x4*)(po + 32 * db + 8 * i) = val;
+                }
+            }
+            if (g == 0) {
+                a.part_ml[2 * prow] = m_run;
+                a.part_ml[2 * prow + 1] = l_tot;
+            }
+        }
+        return;
+    }
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     if (my_q < a.M) {
         float* orow = (float*)a.o + b * a.o_sb + h * a.o_sh + (int64_t)my_q * a.o_sm + 4 * g;
@@ -960,9 +988,55 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a)
     }
 }
 
+// Merge of key-split partial rows: one thread per (head, row, 4 columns).
+// For row i of query tile qt, splits [0, ceil(steps(qt) / split_tiles)) ran;
+// with m* = max_s m_s: O = sum_s 2^(m_s - m*) O_s / sum_s 2^(m_s - m*) l_s, the
+// log-sum-exp merge of attention.cpp:661-674 applied across splits. Rows with
+// no valid key in any split (l = 0) are written as 0.
+template <typename TO>
+__global__ __launch_bounds__(256) void combine_splits_kernel(FwdArgs a) {
+    const int chunks = a.Dv / 4;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t total = (int64_t)a.B * a.H * a.M * chunks;
+    if (idx >= total) return;
+    const int c = (int)(idx % chunks);
+    const int64_t t = idx / chunks;
+    const int row = (int)(t % a.M);
+    const int bh = (int)(t / a.M);
+    const int qt = row / a.split_bm;
+    int steps;
+    if (a.tile_counts != nullptr) {
+        steps = a.tile_counts[qt];
+    } else {
+        const int kend = a.causal ? min(a.N, (qt + 1) * a.split_bm) : a.N;
+        steps = (kend + a.split_bn - 1) / a.split_bn;
+    }
+    const int active = min(a.num_splits, (steps + a.split_tiles - 1) / a.split_tiles);
+    const int64_t stride = (int64_t)a.B * a.H * a.M;
+    const int64_t prow = (int64_t)bh * a.M + row;
+    float m = kNegInf;
+    for (int sp = 0; sp < active; ++sp) m = fmaxf(m, a.part_ml[2 * (sp * stride + prow)]);
+    const float mu = m == kNegInf ? 0.0f : m;
+    float l = 0.0f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < active; ++sp) {
+        const int64_t r = sp * stride + prow;
+        const float w = __builtin_amdgcn_exp2f(a.part_ml[2 * r] - mu);
+        l += w * a.part_ml[2 * r + 1];
+        const f32x4 v = *(const f32x4*)(a.part_o + r * a.Dv + 4 * c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] += w * v[j];
+    }
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const int b = bh / a.H, h = bh - b * a.H;
+    TO* orow = (TO*)a.o + b * a.o_sb + h * a.o_sh + (int64_t)row * a.o_sm + 4 * c;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) orow[j] = (TO)(acc[j] * inv);
+}
+
 template <typename K>
 hipError_t launch(K kernel, int threads, const FwdArgs& a, hipStream_t s, bool paired = false) {
-    const int64_t grid = (int64_t)a.B * a.H * (paired ? (a.num_q_tiles + 1) / 2 : a.num_q_tiles);
+    const int64_t grid = (int64_t)a.B * a.H * (paired ? (a.num_q_tiles + 1) / 2 : a.num_q_tiles) * a.num_splits;
     if (grid <= 0) return hipSuccess;
     hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(threads), 0, s, a);
     return hipGetLastError();
@@ -1009,6 +1083,15 @@ hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipS
                                : launch(flash_fwd_mfma32_kernel<128, false>, kThreads32, a, s);
     }
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_combine_splits(const FwdArgs& a, hipStream_t s) {
+    const int64_t total = (int64_t)a.B * a.H * a.M * (a.Dv / 4);
+    if (total <= 0) return hipSuccess;
+    const dim3 grid((unsigned)((total + 255) / 256));
+    if (a.out_f32) hipLaunchKernelGGL(combine_splits_kernel<float>, grid, dim3(256), 0, s, a);
+    else return hipErrorInvalidValue;  // the key split is used by the fp32 kernel only
+    return hipGetLastError();
 }
 
 const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile_list) {

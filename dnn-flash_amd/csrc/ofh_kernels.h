@@ -52,6 +52,15 @@ struct FwdArgs {
     float softcap;      // 0: off
     float inv_softcap;
     int out_f32;        // 1: O is fp32, else O has the input dtype
+    // Key split: workgroup s of a query tile runs its K/V tile steps
+    // [s*split_tiles, (s+1)*split_tiles) and, when num_splits > 1, writes the
+    // unnormalised O rows and (m, l) per row to part_o / part_ml instead of O;
+    // combine_splits merges them. num_splits == 1: one workgroup per query tile.
+    int num_splits;
+    int split_tiles;
+    int split_bm, split_bn;  // query rows per query tile and keys per K/V tile of the split kernel
+    float* part_o;           // [num_splits][B*H][M][Dv] fp32
+    float* part_ml;          // [num_splits][B*H][M][2] fp32: running max (log2 units), row sum
 };
 
 // Block-mask tile list entry: the key tile index and, for each 32-row slice
@@ -98,6 +107,8 @@ struct QkScoreArgs {
 hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipStream_t s);
 hipError_t launch_rowwise(const FwdArgs& a, int dtype, hipStream_t s);
 hipError_t launch_tile_lists(const TileListArgs& a, hipStream_t s);
+// Merge of the key-split partial rows into O (num_splits > 1).
+hipError_t launch_combine_splits(const FwdArgs& a, hipStream_t s);
 hipError_t launch_qk_score(const QkScoreArgs& a, int dtype, hipStream_t s);
 // Matrix-core score kernel for bf16/fp16 with unit k-strides and 16-byte rows.
 bool qk_score_mfma_supported(const QkScoreArgs& a, int dtype);

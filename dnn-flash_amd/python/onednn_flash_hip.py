@@ -85,6 +85,7 @@ class LaunchInfo(ctypes.Structure):
         ("threads", ctypes.c_int32),
         ("workgroups", ctypes.c_int64),
         ("uses_tile_list", ctypes.c_int32),
+        ("key_splits", ctypes.c_int32),
         ("kernel_name", ctypes.c_char * 96),
     ]
 

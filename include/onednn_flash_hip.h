@@ -111,9 +111,11 @@ typedef struct ofh_attention_params {
  * else zero (no mask, no bias, AUTO). */
 void ofh_attention_params_init(ofh_attention_params* p);
 
-/* Bytes of device scratch the forward call needs for these parameters (the
- * per-query-tile list of allowed key tiles when a block mask is given; 0
- * otherwise). */
+/* Bytes of device scratch the forward call needs for these parameters: the
+ * per-query-tile list of allowed key tiles when a block mask is given, and the
+ * partial rows (unnormalised O, running max and sum) when an fp32 call with few
+ * query tiles splits each query tile's keys over several workgroups (see
+ * ofh_launch_info.key_splits); 0 otherwise. */
 int ofh_attention_workspace_bytes(const ofh_attention_params* p, size_t* bytes);
 
 /* Attention forward on device buffers, ordered on `stream` (asynchronous).
@@ -142,6 +144,8 @@ typedef struct ofh_launch_info {
     int32_t threads;          /* threads per workgroup */
     int64_t workgroups;       /* grid size of the attention kernel */
     int32_t uses_tile_list;   /* 1 when a block-mask tile list is built first */
+    int32_t key_splits;       /* workgroups per query tile, each over a range of K/V
+                                 tiles; > 1 adds a kernel that merges the partial rows */
     char kernel_name[96];
 } ofh_launch_info;
 

@@ -188,6 +188,16 @@ def test_kernel_choice(ofh):
     assert info.workgroups == 4 * 32 * 8 and info.block_m == 256 and info.threads == 512
     info = F.launch_info(F.make_params(4, 32, 4096, 4096, 128, dtype=F.DTYPE_BF16))
     assert info.workgroups == 4 * 32 * 16
+    assert info.key_splits == 1
+    # fp32 with few query tiles: each query tile's keys run as several workgroups
+    p = F.make_params(1, 4, 512, 512, 64, dtype=F.DTYPE_F32)
+    info = F.launch_info(p)
+    assert info.key_splits == 8 and info.workgroups == 4 * 4 * 8
+    assert F.workspace_bytes(p) >= 8 * 4 * 512 * 66 * 4
+    p = F.make_params(2, 8, 2048, 2048, 64, dtype=F.DTYPE_F32, causal=True)
+    assert F.launch_info(p).key_splits == 4
+    p = F.make_params(8, 32, 2048, 2048, 64, dtype=F.DTYPE_F32, causal=True)
+    assert F.launch_info(p).key_splits == 1 and F.workspace_bytes(p) == 0
 
 
 def test_useful_flops_match_workloads(ofh):

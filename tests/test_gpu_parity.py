@@ -200,6 +200,69 @@ def test_explicit_workspace(ofh):
     assert e.value.code == F.OFH_ERROR_WORKSPACE_TOO_SMALL
 
 
+KEY_SPLIT_CASES = {
+    # name: (B, H, M, N, D, causal, extras)
+    "plain": (1, 2, 300, 1000, 64, False, {}),
+    "causal": (1, 2, 1000, 1000, 128, True, {}),
+    "wide_causal": (1, 3, 700, 260, 64, True, {}),
+    "alibi_softcap": (1, 2, 500, 900, 64, True, {"alibi": True, "softcap": 20.0}),
+    "block_mask": (1, 2, 600, 800, 64, True, {"mask": (64, 64)}),
+    "masked_rows": (1, 1, 512, 768, 64, False, {"mask": (128, 64), "zero_qblock": 1}),
+}
+
+
+@pytest.mark.parametrize("name", list(KEY_SPLIT_CASES))
+def test_key_split_fp32(ofh, name):
+    """fp32 calls with few query tiles run each query tile's keys as several
+    workgroups and merge the partial rows (running max, row sum, unnormalised
+    O) in a second kernel; the merged rows meet the fp32 bar, fully masked rows
+    stay 0, and the workspace query covers the partial rows."""
+    F = ofh
+    B, H, M, N, D, causal, ex = KEY_SPLIT_CASES[name]
+    p = F.make_params(B, H, M, N, D, dtype=F.DTYPE_F32, causal=causal)
+    info = F.launch_info(p)
+    assert info.key_splits > 1, f"{name}: expected a key split, got {info.key_splits}"
+    assert F.workspace_bytes(p) >= info.key_splits * B * H * M * (D + 2) * 4
+    dev, host = make_inputs("f32", B, H, M, N, D, seed=len(name))
+    kw, rk = {}, {}
+    if ex.get("alibi"):
+        kw["slopes"] = rk["slopes"] = alibi_slopes(H)
+    if "softcap" in ex:
+        kw["softcap"] = rk["softcap"] = ex["softcap"]
+    if "mask" in ex:
+        mbs = ex["mask"]
+        qb, kb = -(-M // mbs[0]), -(-N // mbs[1])
+        mask = (np.random.default_rng(7).random((qb, kb)) < 0.5).astype(np.uint8)
+        mask[:, 0] = 1
+        if "zero_qblock" in ex:
+            mask[ex["zero_qblock"], :] = 0
+        kw.update(mask=mask, mbs=mbs)
+        rk.update(mask=mask, mbs=mbs)
+    print(f"key split {name}: splits {info.key_splits} workgroups {info.workgroups}", flush=True)
+    out = run(F, dev, dt="f32", causal=causal, **kw)
+    check(out, oracle_full(host, causal=causal, **rk), "f32", f"key split {name}")
+    if "zero_qblock" in ex:
+        z = ex["zero_qblock"] * ex["mask"][0]
+        assert np.all(out[:, :, z:z + ex["mask"][0]] == 0)
+
+
+def test_key_split_workspace(ofh):
+    F = ofh
+    B, H, M, N, D = 1, 2, 256, 1024, 64
+    p = F.make_params(B, H, M, N, D, dtype=F.DTYPE_F32)
+    assert F.launch_info(p).key_splits > 1
+    need = F.workspace_bytes(p)
+    dev, host = make_inputs("f32", B, H, M, N, D, seed=21)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    out = F.attention_fwd(*dev, workspace=ws)
+    torch.cuda.synchronize()
+    check(out.cpu().numpy(), oracle_full(host), "f32", "key split, caller workspace")
+    small = torch.empty(need - 4, dtype=torch.uint8, device="cuda")
+    with pytest.raises(F.OfhError) as e:
+        F.attention_fwd(*dev, workspace=small)
+    assert e.value.code == F.OFH_ERROR_WORKSPACE_TOO_SMALL
+
+
 def test_host_entry_point(ofh):
     F = ofh
     B, H, M, N, D = 1, 2, 100, 130, 64
