@@ -1014,18 +1014,37 @@ __global__ __launch_bounds__(256) void combine_splits_kernel(FwdArgs a) {
     const int active = min(a.num_splits, (steps + a.split_tiles - 1) / a.split_tiles);
     const int64_t stride = (int64_t)a.B * a.H * a.M;
     const int64_t prow = (int64_t)bh * a.M + row;
-    float m = kNegInf;
-    for (int sp = 0; sp < active; ++sp) m = fmaxf(m, a.part_ml[2 * (sp * stride + prow)]);
-    const float mu = m == kNegInf ? 0.0f : m;
-    float l = 0.0f;
+    // One pass in groups of four splits: the loads of a group are independent,
+    // so they are in flight together; the running max is raised per group.
+    constexpr int G = 4;
+    float m = kNegInf, l = 0.0f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int sp = 0; sp < active; ++sp) {
-        const int64_t r = sp * stride + prow;
-        const float w = __builtin_amdgcn_exp2f(a.part_ml[2 * r] - mu);
-        l += w * a.part_ml[2 * r + 1];
-        const f32x4 v = *(const f32x4*)(a.part_o + r * a.Dv + 4 * c);
+    for (int s0 = 0; s0 < active; s0 += G) {
+        float ms[G], ls[G];
+        f32x4 os[G];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[j] += w * v[j];
+        for (int j = 0; j < G; ++j) {
+            const int64_t r = (int64_t)min(s0 + j, active - 1) * stride + prow;
+            ms[j] = s0 + j < active ? a.part_ml[2 * r] : kNegInf;
+            ls[j] = a.part_ml[2 * r + 1];
+            os[j] = *(const f32x4*)(a.part_o + r * a.Dv + 4 * c);
+        }
+        float mg = m;
+#pragma unroll
+        for (int j = 0; j < G; ++j) mg = fmaxf(mg, ms[j]);
+        const float mu = mg == kNegInf ? 0.0f : mg;
+        const float keep = __builtin_amdgcn_exp2f(m - mu);  // 0 while m is -inf
+        l *= keep;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] *= keep;
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const float w = __builtin_amdgcn_exp2f(ms[j] - mu);  // 0 for splits past `active`
+            l += w * ls[j];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[t] += w * os[j][t];
+        }
+        m = mg;
     }
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     const int b = bh / a.H, h = bh - b * a.H;
