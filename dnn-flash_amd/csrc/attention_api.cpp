@@ -88,13 +88,6 @@ void run_host(const float* q, const float* k, const float* v, float* out, size_t
     const size_t off_k = round_up(nq * 4), off_v = off_k + round_up(nk * 4);
     const size_t off_o = off_v + round_up(nv * 4), off_m = off_o + round_up(no * 4);
     const size_t off_b = off_m + round_up(nmask), off_s = off_b + round_up(dense.size() * 4);
-    const size_t total = off_s + round_up(o.alibi_slopes.size() * 4);
-    ws.reserve_device_bytes(total);
-    char* base = static_cast<char*>(ws.device_buffer);
-
-    hip_check(hipMemcpy(base, q, nq * 4, hipMemcpyHostToDevice), "hipMemcpy(q)");
-    hip_check(hipMemcpy(base + off_k, k, nk * 4, hipMemcpyHostToDevice), "hipMemcpy(k)");
-    hip_check(hipMemcpy(base + off_v, v, nv * 4, hipMemcpyHostToDevice), "hipMemcpy(v)");
 
     ofh_attention_params p;
     ofh_attention_params_init(&p);
@@ -110,13 +103,29 @@ void run_host(const float* q, const float* k, const float* v, float* out, size_t
     p.causal = o.causal ? 1 : 0;
     p.algorithm = algorithm;
     if (nmask) {
-        hip_check(hipMemcpy(base + off_m, o.block_mask->allowed.data(), nmask, hipMemcpyHostToDevice),
-                  "hipMemcpy(mask)");
-        p.mask_allowed = reinterpret_cast<const uint8_t*>(base + off_m);
+        p.mask_allowed = o.block_mask->allowed.data();  // host pointer: only the sizes are read here
         p.mask_query_block_size = o.block_mask->query_block_size;
         p.mask_key_block_size = o.block_mask->key_block_size;
         p.mask_query_blocks = o.block_mask->query_blocks;
         p.mask_key_blocks = o.block_mask->key_blocks;
+    }
+    // the attention workspace (tile lists, key-split partial rows) lives in this
+    // thread's buffer too, so that concurrent threads never share one
+    size_t ws_bytes = 0;
+    throw_status(ofh_attention_workspace_bytes(&p, &ws_bytes));
+    const size_t off_w = off_s + round_up(o.alibi_slopes.size() * 4);
+    const size_t total = off_w + round_up(ws_bytes);
+    ws.reserve_device_bytes(total);
+    char* base = static_cast<char*>(ws.device_buffer);
+
+    hip_check(hipMemcpy(base, q, nq * 4, hipMemcpyHostToDevice), "hipMemcpy(q)");
+    hip_check(hipMemcpy(base + off_k, k, nk * 4, hipMemcpyHostToDevice), "hipMemcpy(k)");
+    hip_check(hipMemcpy(base + off_v, v, nv * 4, hipMemcpyHostToDevice), "hipMemcpy(v)");
+
+    if (nmask) {
+        hip_check(hipMemcpy(base + off_m, o.block_mask->allowed.data(), nmask, hipMemcpyHostToDevice),
+                  "hipMemcpy(mask)");
+        p.mask_allowed = reinterpret_cast<const uint8_t*>(base + off_m);
     }
     if (!dense.empty()) {
         hip_check(hipMemcpy(base + off_b, dense.data(), dense.size() * 4, hipMemcpyHostToDevice),
@@ -130,8 +139,8 @@ void run_host(const float* q, const float* k, const float* v, float* out, size_t
         p.alibi_slopes = reinterpret_cast<const float*>(base + off_s);
     }
     p.softcap = o.softcap > 0.0f ? o.softcap : 0.0f;
-    throw_status(ofh_attention_fwd(&p, base, base + off_k, base + off_v, base + off_o, nullptr, 0,
-                                   nullptr));
+    throw_status(ofh_attention_fwd(&p, base, base + off_k, base + off_v, base + off_o,
+                                   ws_bytes ? base + off_w : nullptr, ws_bytes, nullptr));
     hip_check(hipMemcpy(out, base + off_o, no * 4, hipMemcpyDeviceToHost), "hipMemcpy(out)");
 }
 

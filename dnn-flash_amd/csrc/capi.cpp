@@ -446,7 +446,16 @@ int ofh_attention_fwd_host(const ofh_attention_params* p, const float* q, const 
     const size_t off_q = 0, off_k = off_q + up(nq * es), off_v = off_k + up(nk * es);
     const size_t off_o = off_v + up(nv * es), off_m = off_o + up(no * 4);
     const size_t off_b = off_m + up(mask_n), off_a = off_b + up(bias_n * 4);
-    const size_t total = off_a + up(alibi_n * 4);
+    // this thread's own attention workspace (tile lists, key-split partial
+    // rows), so that concurrent host threads never share one
+    size_t ws_n = 0;
+    {
+        ofh_attention_params wp = *p;
+        wp.out_dtype = OFH_DTYPE_F32;
+        if (int rc = ofh_attention_workspace_bytes(&wp, &ws_n)) return rc;
+    }
+    const size_t off_w = off_a + up(alibi_n * 4);
+    const size_t total = off_w + up(ws_n);
 
     int dev = 0;
     OFH_HIP_CHECK(hipGetDevice(&dev));
@@ -489,8 +498,8 @@ int ofh_attention_fwd_host(const ofh_attention_params* p, const float* q, const 
         OFH_HIP_CHECK(hipMemcpy(base + off_a, p->alibi_slopes, alibi_n * 4, hipMemcpyHostToDevice));
         dp.alibi_slopes = reinterpret_cast<const float*>(base + off_a);
     }
-    if (int rc = fwd_impl(&dp, base + off_q, base + off_k, base + off_v, base + off_o, nullptr, 0,
-                          nullptr))
+    if (int rc = fwd_impl(&dp, base + off_q, base + off_k, base + off_v, base + off_o,
+                          ws_n ? base + off_w : nullptr, ws_n, nullptr))
         return rc;
     OFH_HIP_CHECK(hipMemcpy(out, base + off_o, no * 4, hipMemcpyDeviceToHost));
     OFH_HIP_CHECK(hipDeviceSynchronize());

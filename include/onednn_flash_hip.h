@@ -120,7 +120,12 @@ int ofh_attention_workspace_bytes(const ofh_attention_params* p, size_t* bytes);
 
 /* Attention forward on device buffers, ordered on `stream` (asynchronous).
  * workspace may be NULL: the library then uses a per-device buffer it owns,
- * grown on demand (one hipMalloc the first time a larger size is needed).
+ * grown on demand (one hipMalloc the first time a larger size is needed, after
+ * a device synchronisation if an older buffer is replaced). Calls captured
+ * into a HIP graph should pass a workspace of ofh_attention_workspace_bytes
+ * bytes, or follow an uncaptured call of the same shape, so that no growth
+ * happens during capture. Calls sharing the library's buffer must be ordered
+ * (one stream, or synchronised streams).
  * Fully-masked query rows are written as zeros, as standard_attention leaves
  * them (attention.cpp:111-113). */
 int ofh_attention_fwd(const ofh_attention_params* p, const void* q, const void* k,

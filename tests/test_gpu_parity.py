@@ -279,6 +279,48 @@ def test_host_entry_point(ofh):
         check(out, ref, dt, f"host entry {dt}")
 
 
+def test_host_entry_concurrent_threads(ofh):
+    """Host threads calling the host entry at the same time each get their own
+    staging and attention workspace (key-split partial rows, tile lists): every
+    result meets the bar against the oracle of its own inputs."""
+    import threading
+    F = ofh
+    B, H, M, N, D = 1, 2, 256, 768, 64
+    p = F.make_params(B, H, M, N, D, dtype=F.DTYPE_F32)
+    assert F.launch_info(p).key_splits > 1
+    jobs = []
+    for t in range(4):
+        q, k, v = (O.normal(10 * t + s, shp) for s, shp in ((1, (B, H, M, D)), (2, (B, H, N, D)),
+                                                             (3, (B, H, N, D))))
+        jobs.append((q, k, v, np.zeros((B, H, M, D), np.float32)))
+    errors = []
+
+    def work(job):
+        q, k, v, out = job
+        try:
+            for _ in range(5):
+                pp = F.make_params(B, H, M, N, D, dtype=F.DTYPE_F32, causal=True, scale=0.125)
+                F.check(F.lib().ofh_attention_fwd_host(ctypes.byref(pp), q.ctypes.data, k.ctypes.data,
+                                                       v.ctypes.data, out.ctypes.data))
+        except Exception as e:  # reported below, on the main thread
+            errors.append(e)
+
+    refs = [oracle_full((q, k, v), causal=True, scale=0.125) for q, k, v, _ in jobs]
+    for t, job in enumerate(jobs):  # one thread at a time first
+        work(job)
+        assert not errors, errors
+        check(job[3], refs[t], "f32", f"host call {t}, one thread")
+        job[3][:] = 0
+    threads = [threading.Thread(target=work, args=(j,)) for j in jobs]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors, errors
+    for t, job in enumerate(jobs):
+        check(job[3], refs[t], "f32", f"host thread {t}")
+
+
 # ---------------------------------------------------------------------------
 # the five workloads at full size, sampled rows
 
