@@ -3,11 +3,12 @@
 // Replaces the CPU loop nest of flash_attention_qk_pv_tile_ws
 // (src/onednn_flash/attention.cpp:486-695 of the reference) and its batched
 // driver (src/onednn_flash/batched_attention.cpp:9-49): one workgroup owns a
-// 128-row query block of one (batch, head); K/V stream through LDS in tiles
-// of 64 keys (32 for fp32); QK^T and PV run on MFMA; the online-softmax
-// recurrence (running max, rescaled running sum, rescaled accumulator,
-// attention.cpp:628-673) lives in registers; the N x N score matrix is never
-// formed.
+// query block of one (batch, head) (256 rows for bf16/fp16, 128 with a
+// block mask or for fp32), each wavefront 32 of its rows; K/V stream through
+// LDS in tiles of 64 keys (32 for fp32); QK^T and PV run on MFMA; the
+// online-softmax recurrence (running max, rescaled running sum, rescaled
+// accumulator, attention.cpp:628-673) lives in registers; the N x N score
+// matrix is never formed.
 //
 // Layout trick. Scores are computed transposed, S^T = K * Q^T, with K as the
 // MFMA A operand and Q as the B operand. In the 32x32 accumulator layout lane
@@ -15,8 +16,10 @@
 // sum and the accumulator rescale are per-lane scalars, and the only
 // cross-lane step per tile is one exchange between the two 32-lane halves
 // for the max. The output is accumulated transposed as well, O^T = V^T * P^T:
-// the B operand P^T is exactly the lane's own probabilities (no shuffle), and
-// V^T is read from a transposed copy of the V tile kept in LDS.
+// the B operand P^T is exactly the lane's own probabilities (no shuffle). In
+// the 16-bit kernels the V^T A-operand fragments come from the row-major V
+// tile in LDS through the transposing ds_read_b64_tr_b16; the fp32 kernel
+// reads V row-major (one element per lane and operand).
 //
 // The accumulator row r = 8i + 4g + j (lane half g = l/32, register 4i+j)
 // is fed from A-operand row r, and A rows are permuted by kappa(r) =
@@ -794,6 +797,9 @@ __global__ __launch_bounds__(NWAVES * 64, 8 / NWAVES) void flash_fwd_lockstep_ke
 // and operand, so K and V stay row-major in LDS (no transposition): the
 // reduction index d of S^T is split as d = g*D/2 + s over the two lane halves,
 // and each PV step takes the two keys that the lane halves hold in register u.
+// With a key split (FwdArgs::num_splits > 1) the workgroups of a query tile
+// each run a range of its K/V tile steps and write partial rows, which
+// combine_splits_kernel merges.
 
 constexpr int kBlockNF32 = 32;
 constexpr int kWaves32 = 4;
