@@ -8,6 +8,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <limits>
 #include <map>
@@ -175,11 +176,14 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
                          (p->dtype != OFH_DTYPE_F32 || p->out_dtype == OFH_DTYPE_F32) &&
                          aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) &&
                          strides_ok(r.qs, es) && strides_ok(r.ks, es) && strides_ok(r.vs, es) &&
-                         strides_ok(r.os, oes);
+                         strides_ok(r.os, oes) &&
+                         // K/V staging keeps per-lane row offsets (row < 64) in 32 bits
+                         std::llabs((long long)r.ks[2]) <= (1 << 24) && std::llabs((long long)r.vs[2]) <= (1 << 24);
     if (p->algorithm == OFH_ALGO_FLASH_MFMA && !mfma_ok)
         return set_error(OFH_ERROR_UNSUPPORTED,
-                         "flash MFMA kernel needs head_dim == value_dim in {64, 128} and 16-byte "
-                         "aligned rows; use OFH_ALGO_AUTO or OFH_ALGO_ROWWISE");
+                         "flash MFMA kernel needs head_dim == value_dim in {64, 128}, 16-byte "
+                         "aligned rows and K/V token strides of at most 2^24 elements; use "
+                         "OFH_ALGO_AUTO or OFH_ALGO_ROWWISE");
     if (p->algorithm == OFH_ALGO_ROWWISE || !mfma_ok) {
         r.algorithm = OFH_ALGO_ROWWISE;
         if (p->head_dim > 1024)

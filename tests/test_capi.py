@@ -198,6 +198,16 @@ def test_kernel_choice(ofh):
     assert F.launch_info(p).key_splits == 4
     p = F.make_params(8, 32, 2048, 2048, 64, dtype=F.DTYPE_F32, causal=True)
     assert F.launch_info(p).key_splits == 1 and F.workspace_bytes(p) == 0
+    # K/V token strides beyond 2^24 elements: the rowwise kernel (64-bit offsets)
+    p = F.make_params(1, 1, 300, 200, 64, dtype=F.DTYPE_BF16)
+    for i, st in enumerate((64 * 200 * 2, 64 * 200 * 2, 1 << 25)):
+        p.k_strides[i] = st
+        p.v_strides[i] = st
+    p.q_strides[:] = (300 * 64, 300 * 64, 64)
+    p.o_strides[:] = (300 * 64, 300 * 64, 64)
+    assert F.launch_info(p).kernel_name.decode() == "rowwise_fwd_kernel"
+    p.algorithm = F.ALGO_FLASH_MFMA
+    _expect_error(F, p, F.OFH_ERROR_UNSUPPORTED, "token strides")
 
 
 def test_useful_flops_match_workloads(ofh):
