@@ -71,7 +71,7 @@ def check(out, ref, dt, label):
 # ---------------------------------------------------------------------------
 # small shapes, full oracle
 
-SHAPES = [(1, 1), (7, 13), (64, 64), (128, 128), (200, 333), (333, 200)]
+SHAPES = [(1, 1), (7, 13), (64, 64), (128, 128), (200, 333), (333, 200), (1, 2049), (257, 1)]
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
