@@ -201,7 +201,8 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
     }
     r.algorithm = OFH_ALGO_FLASH_MFMA;
     const ofh::MfmaTiles tiles =
-        ofh::flash_mfma_tiles(p->dtype, r.general_mod, p->mask_allowed != nullptr, p->causal != 0);
+        ofh::flash_mfma_tiles(p->dtype, (int)p->head_dim, r.general_mod, p->mask_allowed != nullptr,
+                              p->causal != 0);
     r.block_m = tiles.block_m;
     r.block_n = tiles.block_n;
     r.threads = tiles.threads;

@@ -229,7 +229,8 @@ __device__ __forceinline__ float online_softmax_tile(const FwdArgs& a, f32x16 (&
 // branch) runs on a few tiles per row instead of every tile. The result is
 // exact in real arithmetic: O and l share the same stale max.
 
-constexpr int kBlockN16 = 64;
+constexpr int kBlockN16 = 64;      // keys per K/V tile (16-bit kernels) ...
+constexpr int kBlockN16Wide = 128; // ... and for D = 64 without score_mod or block mask
 constexpr float kRescaleSlack = 8.0f;
 constexpr int kFragAhead = 4;  // LDS fragment reads in flight ahead of the MFMAs (plain scale)
 
@@ -250,7 +251,7 @@ enum ScoreMod { MOD_PLAIN = 0, MOD_GENERAL = 1 };
 // them, i.e. the K/V prefetch) at each use.
 __device__ __forceinline__ void wait_vm_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-template <int D>
+template <int D, int BN>
 struct TileLayout {
     static constexpr int RB = D * 2;              // bytes of one K/V row
     static constexpr int CPR = D / 8;             // 16-byte chunks per row
@@ -260,8 +261,8 @@ struct TileLayout {
     // distinct groups of 4 (stride/16 = 4 mod 8 for D=128, 12 for D=64).
     static constexpr int KSTR = RB + 16;
     static constexpr int VSTR = RB + 64;
-    static constexpr int KTILE = kBlockN16 * KSTR;
-    static constexpr int VTILE = kBlockN16 * VSTR;
+    static constexpr int KTILE = BN * KSTR;
+    static constexpr int VTILE = BN * VSTR;
     static constexpr int STAGE = KTILE + VTILE;   // K tile then V tile
     static __device__ __forceinline__ int kaddr(int row, int chunk) { return row * KSTR + (chunk << 4); }
     static __device__ __forceinline__ int vaddr(int row, int chunk) { return row * VSTR + (chunk << 4); }
@@ -298,12 +299,12 @@ __device__ __forceinline__ constexpr int tile_pos(int sb, int e) { return 32 * s
 // The per-wavefront state and the tile operations of one 32-row wavefront.
 // A "tile step" is identified by its entry: the key tile index, or with a
 // block-mask list (LIST) the list entry (key tile + per-slice bits).
-template <typename T, int D, int MOD, bool LIST, int NTHREADS>
+template <typename T, int D, int MOD, bool LIST, int NTHREADS, int BN_>
 struct Wave32 {
     using M16 = Mfma16<T>;
     using v8 = typename M16::v8;
-    using L = TileLayout<D>;
-    static constexpr int BN = kBlockN16;
+    using L = TileLayout<D, BN_>;
+    static constexpr int BN = BN_;
     static constexpr int CPT = BN * L::CPR / NTHREADS;  // 16-byte chunks per thread per tile
     static constexpr int RSTEP = NTHREADS / L::CPR;      // rows between a thread's chunks
     static_assert(CPT >= 1 && BN * L::CPR % NTHREADS == 0 && NTHREADS % L::CPR == 0,
@@ -716,8 +717,8 @@ struct Wave32 {
 
 // Tile steps of the workgroup's query block: their number and, with a block
 // mask, the list of entries.
-__device__ __forceinline__ void tile_range(const FwdArgs& a, int qt, int block_m, int& ntiles,
-                                           const int*& list) {
+__device__ __forceinline__ void tile_range(const FwdArgs& a, int qt, int block_m, int block_n,
+                                           int& ntiles, const int*& list) {
     list = nullptr;
     if (a.tile_counts != nullptr) {
         ntiles = a.tile_counts[qt];
@@ -725,7 +726,7 @@ __device__ __forceinline__ void tile_range(const FwdArgs& a, int qt, int block_m
     } else {
         const int q0 = qt * block_m;
         const int kend = a.causal ? min(a.N, q0 + block_m) : a.N;
-        ntiles = (kend + kBlockN16 - 1) / kBlockN16;
+        ntiles = (kend + block_n - 1) / block_n;
     }
 }
 
@@ -734,16 +735,16 @@ __device__ __forceinline__ void tile_range(const FwdArgs& a, int qt, int block_m
 // tile it+2 is loaded into registers right after, so its global latency is
 // hidden behind a whole step. With a list, entries are loaded three steps
 // ahead of their use.
-template <typename T, int D, int MOD, bool LIST, int NWAVES>
+template <typename T, int D, int MOD, bool LIST, int NWAVES, int BN>
 __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* smem, int bh, int qt) {
     constexpr int NTHREADS = NWAVES * 64;
     constexpr int BLOCK_M = NWAVES * kQueriesPerWave;
     static_assert(!LIST || NWAVES <= kListSlices, "list entries carry one bit per wavefront");
-    using W = Wave32<T, D, MOD, LIST, NTHREADS>;
+    using W = Wave32<T, D, MOD, LIST, NTHREADS, BN>;
     using L = typename W::L;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     W w(a, smem, bh, qt * BLOCK_M, wave);
-    tile_range(a, qt, BLOCK_M, w.ntiles, w.list);
+    tile_range(a, qt, BLOCK_M, BN, w.ntiles, w.list);
     const int ntiles = w.ntiles;
 
     int e_cur = ntiles > 0 ? w.entry(0) : 0;
@@ -779,16 +780,16 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
     w.store_output();
 }
 
-template <typename T, int D, int MOD, bool LIST, int NWAVES, bool PAIRED>
+template <typename T, int D, int MOD, bool LIST, int NWAVES, bool PAIRED, int BN = kBlockN16>
 __global__ __launch_bounds__(NWAVES * 64, 8 / NWAVES) void flash_fwd_lockstep_kernel(FwdArgs a) {
-    using L = TileLayout<D>;
+    using L = TileLayout<D, BN>;
     __shared__ __attribute__((aligned(16))) unsigned char smem[2 * L::STAGE];
     int bh, qts[2];
     const int n = work_tiles(a, PAIRED, bh, qts);
-    lockstep_qtile<T, D, MOD, LIST, NWAVES>(a, smem, bh, qts[0]);
+    lockstep_qtile<T, D, MOD, LIST, NWAVES, BN>(a, smem, bh, qts[0]);
     if (n > 1) {
         __syncthreads();  // LDS stages are reused
-        lockstep_qtile<T, D, MOD, LIST, NWAVES>(a, smem, bh, qts[1]);
+        lockstep_qtile<T, D, MOD, LIST, NWAVES, BN>(a, smem, bh, qts[1]);
     }
 }
 
@@ -1078,6 +1079,14 @@ static bool pairs_causal_tiles(bool causal, bool tile_list) { return causal && !
 
 static int sched16(bool tile_list) { return tile_list ? SCHED_LOCKSTEP4 : SCHED_LOCKSTEP8; }
 
+// Keys per K/V tile of a 16-bit call: 128 for D = 64 without score_mod or
+// block mask (half the barriers and tile stores per key; measured +9 to +13 %),
+// else 64 (at D = 128 the wider tile spills registers; with a block mask it
+// skips at a coarser grain; the score_mod kernel holds all fragments of a tile).
+static int block_n16(int D, bool general_mod, bool tile_list) {
+    return (D == 64 && !general_mod && !tile_list) ? kBlockN16Wide : kBlockN16;
+}
+
 template <typename T, int D>
 static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
     const bool list = a.tile_counts != nullptr;
@@ -1088,8 +1097,9 @@ static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
     if (general_mod)
         return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8, true>, 512, a, s, true)
                       : launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8, false>, 512, a, s);
-    return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, true>, 512, a, s, true)
-                  : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, false>, 512, a, s);
+    constexpr int BN = D == 64 ? kBlockN16Wide : kBlockN16;  // block_n16(D, false, false)
+    return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, true, BN>, 512, a, s, true)
+                  : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, false, BN>, 512, a, s);
 }
 
 hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipStream_t s) {
@@ -1127,23 +1137,23 @@ const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile
     if (dtype == DT_F32) return f32names[D == 128][general_mod ? 1 : 0];
     // [f16][D==128][score_mod][list]
     static const char* names[2][2][2][2] = {
-        {{{"flash_fwd_lockstep_kernel<bf16,64,plain,8w>", "flash_fwd_lockstep_kernel<bf16,64,plain,list,4w>"},
+        {{{"flash_fwd_lockstep_kernel<bf16,64,plain,8w,128keys>", "flash_fwd_lockstep_kernel<bf16,64,plain,list,4w>"},
           {"flash_fwd_lockstep_kernel<bf16,64,mod,8w>", "flash_fwd_lockstep_kernel<bf16,64,mod,list,4w>"}},
          {{"flash_fwd_lockstep_kernel<bf16,128,plain,8w>", "flash_fwd_lockstep_kernel<bf16,128,plain,list,4w>"},
           {"flash_fwd_lockstep_kernel<bf16,128,mod,8w>", "flash_fwd_lockstep_kernel<bf16,128,mod,list,4w>"}}},
-        {{{"flash_fwd_lockstep_kernel<f16,64,plain,8w>", "flash_fwd_lockstep_kernel<f16,64,plain,list,4w>"},
+        {{{"flash_fwd_lockstep_kernel<f16,64,plain,8w,128keys>", "flash_fwd_lockstep_kernel<f16,64,plain,list,4w>"},
           {"flash_fwd_lockstep_kernel<f16,64,mod,8w>", "flash_fwd_lockstep_kernel<f16,64,mod,list,4w>"}},
          {{"flash_fwd_lockstep_kernel<f16,128,plain,8w>", "flash_fwd_lockstep_kernel<f16,128,plain,list,4w>"},
           {"flash_fwd_lockstep_kernel<f16,128,mod,8w>", "flash_fwd_lockstep_kernel<f16,128,mod,list,4w>"}}}};
     return names[dtype == DT_F16][D == 128][general_mod ? 1 : 0][tile_list ? 1 : 0];
 }
 
-MfmaTiles flash_mfma_tiles(int dtype, bool general_mod, bool tile_list, bool causal) {
-    (void)general_mod;
+MfmaTiles flash_mfma_tiles(int dtype, int D, bool general_mod, bool tile_list, bool causal) {
     if (dtype == DT_F32) return MfmaTiles{kBlockM32, kBlockNF32, kThreads32, false};
     const bool paired = pairs_causal_tiles(causal, tile_list);
-    if (sched16(tile_list) == SCHED_LOCKSTEP4) return MfmaTiles{128, kBlockN16, 256, paired};
-    return MfmaTiles{256, kBlockN16, 512, paired};
+    const int bn = block_n16(D, general_mod, tile_list);
+    if (sched16(tile_list) == SCHED_LOCKSTEP4) return MfmaTiles{128, bn, 256, paired};
+    return MfmaTiles{256, bn, 512, paired};
 }
 
 }  // namespace ofh

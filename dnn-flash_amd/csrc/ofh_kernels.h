@@ -116,6 +116,6 @@ hipError_t launch_qk_score_mfma(const QkScoreArgs& a, int dtype, hipStream_t s);
 
 const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile_list);
 // Workgroup tiling of the MFMA kernel for a dtype.
-MfmaTiles flash_mfma_tiles(int dtype, bool general_mod, bool tile_list, bool causal);
+MfmaTiles flash_mfma_tiles(int dtype, int head_dim, bool general_mod, bool tile_list, bool causal);
 
 }  // namespace ofh
