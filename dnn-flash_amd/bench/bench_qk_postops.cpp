@@ -448,8 +448,8 @@ void write_csv(const std::string& path, const std::vector<Record>& recs) {
 }  // namespace
 
 int main(int argc, char** argv) {
-    std::string json_path = "gpurun_out/qk_postops/cpp-qk-postops.json";
-    std::string csv_path = "gpurun_out/qk_postops/cpp-qk-postops.csv";
+    std::string json_path = "results/qk_postops/cpp-qk-postops.json";
+    std::string csv_path = "results/qk_postops/cpp-qk-postops.csv";
     int warmup = 2, repeat = 5;
     bool include_deferred = false, large = false, large_only = false;
     for (int i = 1; i < argc; ++i) {
