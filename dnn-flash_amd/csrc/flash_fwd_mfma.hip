@@ -299,15 +299,16 @@ __device__ __forceinline__ constexpr int tile_pos(int sb, int e) { return 32 * s
 // The per-wavefront state and the tile operations of one 32-row wavefront.
 // A "tile step" is identified by its entry: the key tile index, or with a
 // block-mask list (LIST) the list entry (key tile + per-slice bits).
-template <typename T, int D, int MOD, bool LIST, int NTHREADS, int BN_>
+template <typename T, int D, int MOD, bool LIST, int NTHREADS, int BN_, int SB = 1>
 struct Wave32 {
     using M16 = Mfma16<T>;
     using v8 = typename M16::v8;
-    using L = TileLayout<D, BN_>;
+    using L = TileLayout<D, BN_ * SB>;
     static constexpr int BN = BN_;
-    static constexpr int CPT = BN * L::CPR / NTHREADS;  // 16-byte chunks per thread per tile
+    static constexpr int SN = BN_ * SB;                 // keys per staged tile
+    static constexpr int CPT = SN * L::CPR / NTHREADS;  // 16-byte chunks per thread per tile
     static constexpr int RSTEP = NTHREADS / L::CPR;      // rows between a thread's chunks
-    static_assert(CPT >= 1 && BN * L::CPR % NTHREADS == 0 && NTHREADS % L::CPR == 0,
+    static_assert(CPT >= 1 && SN * L::CPR % NTHREADS == 0 && NTHREADS % L::CPR == 0,
                   "tile must split evenly");
 
     const FwdArgs& a;
@@ -393,11 +394,11 @@ struct Wave32 {
     // uniform tile base plus fixed 32-bit lane offsets; in the last, ragged
     // tile rows past N are clamped to N-1.
     __device__ __forceinline__ void load_tile(int kt) {
-        const int k0 = kt * BN;
+        const int k0 = kt * SN;
         staged_kt = kt;
         const T* kt_base = Kp + (int64_t)k0 * a.k_sn;
         const T* vt_base = Vp + (int64_t)k0 * a.v_sn;
-        if (k0 + BN <= a.N) {
+        if (k0 + SN <= a.N) {
 #pragma unroll
             for (int u = 0; u < CPT; ++u) {
                 kreg[u] = *(const u32x4*)(kt_base + (int64_t)u * RSTEP * a.k_sn + ld_koff);
@@ -415,7 +416,7 @@ struct Wave32 {
     }
     __device__ __forceinline__ void store_tile(int stage_off) {
         unsigned char* base = smem + stage_off;
-        const int k0 = staged_kt * BN;
+        const int k0 = staged_kt * SN;
         // V chunk of the same (row, column): after the K tile, with the V row stride
         const int st_voff = st_koff + L::KTILE + ld_row * (L::VSTR - L::KSTR);
 #pragma unroll
@@ -428,8 +429,8 @@ struct Wave32 {
 
     // S^T = K Q^T for the tile in LDS stage `stage_off`. With a score_mod
     // (longer softmax) all K fragments are read before the first MFMA.
-    __device__ __forceinline__ void qk(int stage_off) {
-        const lds_u8* kb = (const lds_u8*)smem + stage_off + k_lane_off;
+    __device__ __forceinline__ void qk(int stage_off, int sub = 0) {
+        const lds_u8* kb = (const lds_u8*)smem + stage_off + k_lane_off + sub * BN * L::KSTR;
         if (MOD == MOD_GENERAL) {
             v8 kf[BN / 32][D / 16];
 #pragma unroll
@@ -470,8 +471,8 @@ struct Wave32 {
     // O^T += V^T P^T for the tile in LDS stage `stage_off` (A operand from two
     // transposed 4-key reads). With a score_mod all V^T fragments are read
     // before the first MFMA.
-    __device__ __forceinline__ void pv(int stage_off) {
-        const lds_u8* vb = (const lds_u8*)smem + stage_off + v_lane_off;
+    __device__ __forceinline__ void pv(int stage_off, int sub = 0) {
+        const lds_u8* vb = (const lds_u8*)smem + stage_off + v_lane_off + sub * BN * L::VSTR;
         auto vfrag = [&](int c, int db) {
             const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (lds_i16x4*)(vb + (16 * c) * L::VSTR + 64 * db));
@@ -735,15 +736,49 @@ __device__ __forceinline__ void tile_range(const FwdArgs& a, int qt, int block_m
 // tile it+2 is loaded into registers right after, so its global latency is
 // hidden behind a whole step. With a list, entries are loaded three steps
 // ahead of their use.
-template <typename T, int D, int MOD, bool LIST, int NWAVES, int BN>
+template <typename T, int D, int MOD, bool LIST, int NWAVES, int BN, int SB = 1>
 __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* smem, int bh, int qt) {
     constexpr int NTHREADS = NWAVES * 64;
     constexpr int BLOCK_M = NWAVES * kQueriesPerWave;
     static_assert(!LIST || NWAVES <= kListSlices, "list entries carry one bit per wavefront");
-    using W = Wave32<T, D, MOD, LIST, NTHREADS, BN>;
+    using W = Wave32<T, D, MOD, LIST, NTHREADS, BN, SB>;
     using L = typename W::L;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     W w(a, smem, bh, qt * BLOCK_M, wave);
+    if constexpr (SB > 1) {
+        // SB compute steps of BN keys per staged tile of SB*BN keys (one
+        // barrier per staged tile); plain scale without a list only.
+        static_assert(!LIST && MOD == MOD_PLAIN, "sub-steps: plain scale, no list");
+        const int q0 = qt * BLOCK_M;
+        const int kend = a.causal ? min(a.N, q0 + BLOCK_M) : a.N;
+        const int nst = (kend + W::SN - 1) / W::SN;      // staged tiles
+        if (nst > 0) w.load_tile(0);
+        wait_vm_loads();
+        if (nst > 0) w.store_tile(0);
+        if (nst > 1) w.load_tile(1);
+        __syncthreads();
+        for (int st = 0; st < nst; ++st) {
+            const int stage = (st & 1) * L::STAGE;
+#pragma unroll
+            for (int j = 0; j < SB; ++j) {
+                const int e = st * SB + j;               // BN-key compute tile
+                if (e * BN < kend && w.tile_active(e)) {
+                    __builtin_amdgcn_s_setprio(1);
+                    w.qk(stage, j);
+                    __builtin_amdgcn_s_setprio(0);
+                    w.softmax(e);
+                    __builtin_amdgcn_s_setprio(1);
+                    w.pv(stage, j);
+                    __builtin_amdgcn_s_setprio(0);
+                }
+            }
+            if (st + 1 < nst) w.store_tile(((st + 1) & 1) * L::STAGE);
+            if (st + 2 < nst) w.load_tile(st + 2);
+            __syncthreads();
+        }
+        w.store_output();
+        return;
+    }
     tile_range(a, qt, BLOCK_M, BN, w.ntiles, w.list);
     const int ntiles = w.ntiles;
 
@@ -780,16 +815,16 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
     w.store_output();
 }
 
-template <typename T, int D, int MOD, bool LIST, int NWAVES, bool PAIRED, int BN = kBlockN16>
+template <typename T, int D, int MOD, bool LIST, int NWAVES, bool PAIRED, int BN = kBlockN16, int SB = 1>
 __global__ __launch_bounds__(NWAVES * 64, 8 / NWAVES) void flash_fwd_lockstep_kernel(FwdArgs a) {
-    using L = TileLayout<D, BN>;
+    using L = TileLayout<D, BN * SB>;
     __shared__ __attribute__((aligned(16))) unsigned char smem[2 * L::STAGE];
     int bh, qts[2];
     const int n = work_tiles(a, PAIRED, bh, qts);
-    lockstep_qtile<T, D, MOD, LIST, NWAVES, BN>(a, smem, bh, qts[0]);
+    lockstep_qtile<T, D, MOD, LIST, NWAVES, BN, SB>(a, smem, bh, qts[0]);
     if (n > 1) {
         __syncthreads();  // LDS stages are reused
-        lockstep_qtile<T, D, MOD, LIST, NWAVES, BN>(a, smem, bh, qts[1]);
+        lockstep_qtile<T, D, MOD, LIST, NWAVES, BN, SB>(a, smem, bh, qts[1]);
     }
 }
 
@@ -1079,12 +1114,14 @@ static bool pairs_causal_tiles(bool causal, bool tile_list) { return causal && !
 
 static int sched16(bool tile_list) { return tile_list ? SCHED_LOCKSTEP4 : SCHED_LOCKSTEP8; }
 
-// Keys per K/V tile of a 16-bit call: 128 for D = 64 without score_mod or
-// block mask (half the barriers and tile stores per key; measured +9 to +13 %),
-// else 64 (at D = 128 the wider tile spills registers; with a block mask it
-// skips at a coarser grain; the score_mod kernel holds all fragments of a tile).
-static int block_n16(int D, bool general_mod, bool tile_list) {
-    return (D == 64 && !general_mod && !tile_list) ? kBlockN16Wide : kBlockN16;
+// Keys per staged K/V tile (one barrier each) of a 16-bit call: 128 without
+// score_mod or block mask (half the barriers and tile stores per key), else 64
+// (with a block mask a wider tile skips at a coarser grain; the score_mod
+// kernel holds all fragments of a tile). At D = 64 the 128 keys are one compute
+// step (+9 to +13 %); at D = 128, where S and P for 128 keys would spill, they
+// are computed in two 64-key steps between the same barriers (+1 to +5 %).
+static int block_n16(bool general_mod, bool tile_list) {
+    return (!general_mod && !tile_list) ? kBlockN16Wide : kBlockN16;
 }
 
 template <typename T, int D>
@@ -1097,9 +1134,11 @@ static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
     if (general_mod)
         return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8, true>, 512, a, s, true)
                       : launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8, false>, 512, a, s);
-    constexpr int BN = D == 64 ? kBlockN16Wide : kBlockN16;  // block_n16(D, false, false)
-    return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, true, BN>, 512, a, s, true)
-                  : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, false, BN>, 512, a, s);
+    // D = 64: 128-key tiles; D = 128: 128 keys staged per barrier, two 64-key compute steps (block_n16)
+    constexpr int BN = D == 64 ? kBlockN16Wide : kBlockN16;
+    constexpr int SB = D == 64 ? 1 : kBlockN16Wide / kBlockN16;
+    return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, true, BN, SB>, 512, a, s, true)
+                  : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, false, BN, SB>, 512, a, s);
 }
 
 hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipStream_t s) {
@@ -1139,11 +1178,11 @@ const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile
     static const char* names[2][2][2][2] = {
         {{{"flash_fwd_lockstep_kernel<bf16,64,plain,8w,128keys>", "flash_fwd_lockstep_kernel<bf16,64,plain,list,4w>"},
           {"flash_fwd_lockstep_kernel<bf16,64,mod,8w>", "flash_fwd_lockstep_kernel<bf16,64,mod,list,4w>"}},
-         {{"flash_fwd_lockstep_kernel<bf16,128,plain,8w>", "flash_fwd_lockstep_kernel<bf16,128,plain,list,4w>"},
+         {{"flash_fwd_lockstep_kernel<bf16,128,plain,8w,2x64keys>", "flash_fwd_lockstep_kernel<bf16,128,plain,list,4w>"},
           {"flash_fwd_lockstep_kernel<bf16,128,mod,8w>", "flash_fwd_lockstep_kernel<bf16,128,mod,list,4w>"}}},
         {{{"flash_fwd_lockstep_kernel<f16,64,plain,8w,128keys>", "flash_fwd_lockstep_kernel<f16,64,plain,list,4w>"},
           {"flash_fwd_lockstep_kernel<f16,64,mod,8w>", "flash_fwd_lockstep_kernel<f16,64,mod,list,4w>"}},
-         {{"flash_fwd_lockstep_kernel<f16,128,plain,8w>", "flash_fwd_lockstep_kernel<f16,128,plain,list,4w>"},
+         {{"flash_fwd_lockstep_kernel<f16,128,plain,8w,2x64keys>", "flash_fwd_lockstep_kernel<f16,128,plain,list,4w>"},
           {"flash_fwd_lockstep_kernel<f16,128,mod,8w>", "flash_fwd_lockstep_kernel<f16,128,mod,list,4w>"}}}};
     return names[dtype == DT_F16][D == 128][general_mod ? 1 : 0][tile_list ? 1 : 0];
 }
@@ -1151,7 +1190,8 @@ const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile
 MfmaTiles flash_mfma_tiles(int dtype, int D, bool general_mod, bool tile_list, bool causal) {
     if (dtype == DT_F32) return MfmaTiles{kBlockM32, kBlockNF32, kThreads32, false};
     const bool paired = pairs_causal_tiles(causal, tile_list);
-    const int bn = block_n16(D, general_mod, tile_list);
+    (void)D;
+    const int bn = block_n16(general_mod, tile_list);
     if (sched16(tile_list) == SCHED_LOCKSTEP4) return MfmaTiles{128, bn, 256, paired};
     return MfmaTiles{256, bn, 512, paired};
 }

@@ -166,7 +166,7 @@ def test_null_pointers_rejected_before_any_device_work(ofh):
 def test_kernel_choice(ofh):
     F = ofh
     cases = [
-        (dict(dtype=F.DTYPE_BF16, head_dim=128), "flash_fwd_lockstep_kernel<bf16,128,plain,8w>"),
+        (dict(dtype=F.DTYPE_BF16, head_dim=128), "flash_fwd_lockstep_kernel<bf16,128,plain,8w,2x64keys>"),
         (dict(dtype=F.DTYPE_F16, head_dim=64), "flash_fwd_lockstep_kernel<f16,64,plain,8w,128keys>"),
         (dict(dtype=F.DTYPE_F32, head_dim=64), "flash_fwd_mfma32_kernel<64,plain>"),
         (dict(dtype=F.DTYPE_BF16, head_dim=128, softcap=50.0),
@@ -188,8 +188,8 @@ def test_kernel_choice(ofh):
     assert info.workgroups == 4 * 32 * 8 and info.block_m == 256 and info.threads == 512
     info = F.launch_info(F.make_params(4, 32, 4096, 4096, 128, dtype=F.DTYPE_BF16))
     assert info.workgroups == 4 * 32 * 16
-    assert info.key_splits == 1 and info.block_n == 64
-    # D = 64 without score_mod or block mask: 128-key tiles
+    assert info.key_splits == 1 and info.block_n == 128   # staged keys per barrier (2 x 64 computed)
+    # without score_mod or block mask: 128 keys per staged tile
     assert F.launch_info(F.make_params(1, 2, 300, 200, 64, dtype=F.DTYPE_BF16)).block_n == 128
     assert F.launch_info(F.make_params(1, 2, 300, 200, 64, dtype=F.DTYPE_BF16, softcap=5.0)).block_n == 64
     # fp32 with few query tiles: each query tile's keys run as several workgroups
