@@ -126,7 +126,7 @@ int validate(const ofh_attention_params* p, bool check_ptrs, const void* q, cons
 // workgroup). A call with fewer query-tile workgroups than two per CU leaves
 // the chip idle, and causal calls are bound by their longest query tile; such
 // calls run the K/V tile steps of each query tile in ranges of split_tiles
-// (at least two) sized so that all ranges together fill about 512 workgroups,
+// (at least 64 keys) sized so that all ranges together fill about 512 workgroups,
 // then merge the partial rows. Without a mask the tile steps of query tile qt
 // are known on the host; with a block mask the list can only remove steps, so
 // the unmasked count is an upper bound.
@@ -148,7 +148,8 @@ void choose_key_splits(const ofh_attention_params* p, Resolved& r) {
         max_steps = std::max(max_steps, steps);
     }
     total *= bh;
-    const int per = (int)std::max<int64_t>(2, (total + kTargetWorkgroups - 1) / kTargetWorkgroups);
+    const int min_steps = std::max(1, 64 / r.block_n);  // at least 64 keys per split
+    const int per = (int)std::max<int64_t>(min_steps, (total + kTargetWorkgroups - 1) / kTargetWorkgroups);
     int splits = (max_steps + per - 1) / per;
     if (splits <= 1) return;
     splits = std::min(splits, kMaxSplits);

@@ -837,14 +837,15 @@ __global__ __launch_bounds__(NWAVES * 64, 8 / NWAVES) void flash_fwd_lockstep_ke
 // each run a range of its K/V tile steps and write partial rows, which
 // combine_splits_kernel merges.
 
-constexpr int kBlockNF32 = 32;
+constexpr int kBlockNF32 = 32;  // keys per accumulator block of the fp32 kernel
+constexpr int kTilesF32 = 2;    // blocks per K/V tile: 64 keys per barrier (+3 to +5 % over one block)
 constexpr int kWaves32 = 4;
 constexpr int kThreads32 = kWaves32 * 64;
 constexpr int kBlockM32 = kWaves32 * kQueriesPerWave;  // 128
 
-template <int D, bool GENERAL>
+template <int D, bool GENERAL, int NB = 1>
 __global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a) {
-    constexpr int BN = kBlockNF32;
+    constexpr int BN = kBlockNF32 * NB;  // NB blocks of 32 keys per K/V tile
     constexpr int KSTR = D + 4;  // floats; conflict-free 16-byte reads of rows kappa(r)
     constexpr int VSTR = D + 4;  // floats; lane halves read rows 8 apart -> opposite bank halves
     constexpr int KTILE = BN * KSTR;
@@ -965,27 +966,34 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a)
         if (active) {
             const bool need_mask = ((k0 + BN > a.N) || (a.causal && k0 + BN - 1 > qw0)) ||
                                    (list != nullptr && !list_full(ent, wave));
-            f32x16 s[1];
-            s[0] = f32x16{};
+            f32x16 s[NB];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) s[b] = f32x16{};
             const float* krow = Ks + kappa(r) * KSTR + g * (D / 2);
 #pragma unroll
             for (int c = 0; c < D / 8; ++c) {
-                const f32x4 kv = *(const f32x4*)(krow + 4 * c);
+                f32x4 kv[NB];
+#pragma unroll
+                for (int b = 0; b < NB; ++b) kv[b] = *(const f32x4*)(krow + 32 * b * KSTR + 4 * c);
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
-                    s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[t], qf[4 * c + t], s[0], 0, 0, 0);
+#pragma unroll
+                    for (int b = 0; b < NB; ++b)
+                        s[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[b][t], qf[4 * c + t], s[b], 0, 0, 0);
             }
-            const float alpha = online_softmax_tile<1, GENERAL>(a, s, need_mask, my_q, k0, g, slope,
-                                                                bias_row, m_run, l_run);
+            const float alpha = online_softmax_tile<NB, GENERAL>(a, s, need_mask, my_q, k0, g, slope,
+                                                                 bias_row, m_run, l_run);
 #pragma unroll
             for (int db = 0; db < D / 32; ++db) o[db] *= alpha;
 #pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                const float* vrow = Vs + acc_pos(u, g) * VSTR + r;
+            for (int b = 0; b < NB; ++b)
 #pragma unroll
-                for (int db = 0; db < D / 32; ++db)
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * db], s[0][u], o[db], 0, 0, 0);
-            }
+                for (int u = 0; u < 16; ++u) {
+                    const float* vrow = Vs + (32 * b + acc_pos(u, g)) * VSTR + r;
+#pragma unroll
+                    for (int db = 0; db < D / 32; ++db)
+                        o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * db], s[b][u], o[db], 0, 0, 0);
+                }
         }
         if (it + 1 < it1) store_tile((it + 1 - it0) & 1);
         __syncthreads();
@@ -1150,11 +1158,11 @@ hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipS
         if (a.D == 128) return launch16<_Float16, 128>(a, general_mod, s);
     } else if (dtype == DT_F32) {
         if (a.D == 64)
-            return general_mod ? launch(flash_fwd_mfma32_kernel<64, true>, kThreads32, a, s)
-                               : launch(flash_fwd_mfma32_kernel<64, false>, kThreads32, a, s);
+            return general_mod ? launch(flash_fwd_mfma32_kernel<64, true, kTilesF32>, kThreads32, a, s)
+                               : launch(flash_fwd_mfma32_kernel<64, false, kTilesF32>, kThreads32, a, s);
         if (a.D == 128)
-            return general_mod ? launch(flash_fwd_mfma32_kernel<128, true>, kThreads32, a, s)
-                               : launch(flash_fwd_mfma32_kernel<128, false>, kThreads32, a, s);
+            return general_mod ? launch(flash_fwd_mfma32_kernel<128, true, kTilesF32>, kThreads32, a, s)
+                               : launch(flash_fwd_mfma32_kernel<128, false, kTilesF32>, kThreads32, a, s);
     }
     return hipErrorInvalidValue;
 }
@@ -1188,7 +1196,7 @@ const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile
 }
 
 MfmaTiles flash_mfma_tiles(int dtype, int D, bool general_mod, bool tile_list, bool causal) {
-    if (dtype == DT_F32) return MfmaTiles{kBlockM32, kBlockNF32, kThreads32, false};
+    if (dtype == DT_F32) return MfmaTiles{kBlockM32, kBlockNF32 * kTilesF32, kThreads32, false};
     const bool paired = pairs_causal_tiles(causal, tile_list);
     (void)D;
     const int bn = block_n16(general_mod, tile_list);
