@@ -129,6 +129,23 @@ def test_block_masks(ofh, dt):
             check(out, ref, dt, f"{dt} mask {mbs} causal={causal}")
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_block_mask_long_key_ranges(ofh, dt):
+    """Block-mask tile lists over a few thousand and over 1,100 key tiles
+    (entries far beyond one list round of the list kernel)."""
+    rng = np.random.default_rng(31)
+    for M, N in [(300, 4000), (96, 1100 * 64)]:
+        mbs = (64, 64)
+        qb, kb = -(-M // mbs[0]), -(-N // mbs[1])
+        mask = (rng.random((qb, kb)) < 0.3).astype(np.uint8)
+        mask[:, 0] = 1
+        dev, host = make_inputs(dt, 1, 2, M, N, 64, seed=N)
+        for causal in (False, True):
+            out = run(ofh, dev, dt=dt, causal=causal, mask=mask, mbs=mbs)
+            check(out, oracle_full(host, causal=causal, mask=mask, mbs=mbs), dt,
+                  f"{dt} block mask M{M} N{N} causal={causal}")
+
+
 def test_fully_masked_rows_are_zero(ofh):
     M, N, D = 256, 256, 128
     dev, host = make_inputs("bf16", 1, 2, M, N, D, seed=12)
