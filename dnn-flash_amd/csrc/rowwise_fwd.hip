@@ -151,8 +151,9 @@ hipError_t launch_rowwise(const FwdArgs& a, int dtype, hipStream_t s) {
 // attention kernel), whether the slice has an allowed pair at all (else that
 // wavefront skips the tile) and whether the mask allows all of its pairs
 // (else it masks element-wise). Built before the attention launch, so skipped
-// tiles issue no loads at all. One wavefront per query tile; the list is
-// compacted in order with a ballot prefix count.
+// tiles issue no loads at all. One workgroup of four wavefronts per query
+// tile, 256 key tiles per round; the list is compacted in key order with a
+// per-wavefront ballot and a prefix over the wavefronts' counts.
 namespace {
 
 // Rows [q0,q1) x keys [k0,k1), already clipped to the problem. any: some pair
@@ -176,13 +177,17 @@ __device__ void classify_slice(const TileListArgs& a, int q0, int q1, int k0, in
     }
 }
 
-__global__ __launch_bounds__(64) void tile_list_kernel(TileListArgs a) {
-    const int qt = blockIdx.x, lane = threadIdx.x;
+constexpr int kListWaves = 4;
+
+__global__ __launch_bounds__(64 * kListWaves) void tile_list_kernel(TileListArgs a) {
+    const int qt = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    __shared__ int wave_counts[kListWaves];
     const int q0 = qt * a.block_m;
     const int slices = a.block_m / 32;
     int count = 0;
-    for (int base = 0; base < a.num_k_tiles; base += 64) {
-        const int kt = base + lane;
+    for (int base = 0; base < a.num_k_tiles; base += 64 * kListWaves) {
+        const int kt = base + tid;
         unsigned any_bits = 0, full_bits = 0;
         if (kt < a.num_k_tiles) {
             const int k0 = kt * a.block_n;
@@ -197,19 +202,27 @@ __global__ __launch_bounds__(64) void tile_list_kernel(TileListArgs a) {
             }
         }
         const unsigned long long bal = __ballot(any_bits != 0);
-        const int pos = count + __popcll(bal & ((1ull << lane) - 1ull));
+        if (lane == 0) wave_counts[wave] = __popcll(bal);
+        __syncthreads();
+        int before = count, total = count;
+        for (int w = 0; w < kListWaves; ++w) {
+            before += w < wave ? wave_counts[w] : 0;
+            total += wave_counts[w];
+        }
         if (any_bits != 0)
-            a.entries[(int64_t)qt * a.num_k_tiles + pos] = list_entry(kt, any_bits, full_bits);
-        count += __popcll(bal);
+            a.entries[(int64_t)qt * a.num_k_tiles + before + __popcll(bal & ((1ull << lane) - 1ull))] =
+                list_entry(kt, any_bits, full_bits);
+        __syncthreads();  // wave_counts is rewritten in the next round
+        count = total;
     }
-    if (lane == 0) a.counts[qt] = count;
+    if (tid == 0) a.counts[qt] = count;
 }
 
 }  // namespace
 
 hipError_t launch_tile_lists(const TileListArgs& a, hipStream_t s) {
     if (a.num_q_tiles <= 0) return hipSuccess;
-    hipLaunchKernelGGL(tile_list_kernel, dim3(a.num_q_tiles), dim3(64), 0, s, a);
+    hipLaunchKernelGGL(tile_list_kernel, dim3(a.num_q_tiles), dim3(64 * kListWaves), 0, s, a);
     return hipGetLastError();
 }
 
