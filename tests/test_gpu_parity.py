@@ -339,6 +339,35 @@ def test_host_entry_concurrent_threads(ofh):
 
 
 # ---------------------------------------------------------------------------
+# tensors beyond 2^31 elements: head offsets past the 32-bit index range
+
+def test_tensors_beyond_int32_elements(ofh):
+    """B1 H130 N131072 D128 bf16 causal: 2^24 elements per head, so heads 128
+    and 129 start at element offsets >= 2^31 (4.4 GB per tensor). Sampled rows
+    of heads 0, 128 and 129 (first, last and random rows) against the oracle."""
+    B, H, N, D = 1, 130, 131072, 128
+    assert H * N * D > 2**31
+    gen = torch.Generator(device="cuda").manual_seed(31)
+    q, k, v = (torch.randn(B, H, N, D, generator=gen, device="cuda", dtype=torch.bfloat16)
+               for _ in range(3))
+    scale = 1.0 / math.sqrt(D)
+    out = ofh.attention_fwd(q, k, v, scale=scale, causal=True, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    heads = [0, 128, 129]
+    rng = np.random.default_rng(31)
+    rows = np.concatenate([[0, 1, N - 1], rng.choice(N, size=13, replace=False)])
+    host = [t[0, heads].float().cpu().numpy()[None] for t in (q, k, v)]
+    got = out[0, heads][:, torch.from_numpy(rows).cuda()].float().cpu().numpy()
+    del q, k, v, out
+    torch.cuda.empty_cache()
+    prob = O.Problem(1, len(heads), N, N, D, D, scale=scale, causal=True)
+    hidx = np.repeat(np.arange(len(heads)), len(rows))
+    ridx = np.tile(rows, len(heads))
+    ref = O.standard_attention_rows(host[0], host[1], host[2], prob, hidx, ridx, threads=THREADS)
+    check(got.reshape(-1, D), ref, "bf16", f"B{B} H{H} N{N} D{D} heads {heads}")
+
+
+# ---------------------------------------------------------------------------
 # the five workloads at full size, sampled rows
 
 def _sampled_check(F, w, rows_per_head=48, heads=8, seed=100):
