@@ -155,8 +155,8 @@ def cpu_baseline(w, threads: int, nheads: int, min_seconds: float = 10.0):
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU: the attention kernel shards by heads "
-                                   "with no communication; --gpus must be 1"}))
+        print(json.dumps({"error": "the attention library runs on one GPU per process: the kernel "
+                                   "shards by heads with no communication; --gpus must be 1"}))
         return 2
 
     if args.copy_calibration:

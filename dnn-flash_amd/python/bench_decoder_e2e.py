@@ -18,7 +18,7 @@ replays a captured HIP graph of the call (the counterpart of tf.function).
 Times are per call, device-resident, measured with HIP events.
 
     python dnn-flash_amd/python/bench_decoder_e2e.py --seq 4096 --heads 32 --head-dim 128 \\
-        --dtype bf16 --graph --output-json gpurun_out/e2e.json
+        --dtype bf16 --graph --output-json results/e2e.json
 """
 
 from __future__ import annotations

@@ -2,8 +2,8 @@
  * CPU oracle for the Flash-style attention forward path.
  *
  * TEST INFRASTRUCTURE ONLY. Nothing in the shipped library links, loads or
- * calls this code; it is the checker that the HIP kernels are compared with,
- * and the CPU baseline that bench.py times beside them.
+ * calls this code; the tests compare the HIP kernels with it, and bench.py
+ * times it as the CPU baseline beside them.
  *
  * It restates, in plain C++ with the same floating-point operation order, the
  * reference's CPU attention (paths relative to the reference repository):

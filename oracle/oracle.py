@@ -2,7 +2,7 @@
 reference (oracle/_ref/libonednn_flash_ref.so).
 
 TEST INFRASTRUCTURE ONLY. Imported by tests/, by __graft_entry__.smoke() and by
-bench.py's cpu_baseline leg, always as the checker or the timed CPU baseline,
+bench.py's cpu_baseline leg, always as the oracle or the timed CPU baseline,
 never as the product path. The product library never loads it.
 """
 

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/oracle.cpp) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/oracle.cpp) before the GPU tests compare against it.
 
 1. Golden vectors written by the compiled reference (tests/golden/*.npz):
    standard_attention and flash_attention_qk_pv_tile_ws, bit for bit.

@@ -1,6 +1,6 @@
 """The QK score tile oracle (oracle_qk_score_tile, a restatement of
 src/onednn_flash/qk_score_tile.cpp:48-69 over tile_kernel.cpp:67-86), pinned
-before it is used as the checker of the GPU kernels:
+before the GPU kernels are compared with it:
   - bit for bit against the reference's own outputs (tests/golden/qk_score.npz,
     written by tests/golden/make_qk_golden.py from the compiled reference) and,
     where the reference is built here, against it live on strided views;
