@@ -5,7 +5,7 @@
 // driver (src/onednn_flash/batched_attention.cpp:9-49): one workgroup owns a
 // query block of one (batch, head) (256 rows for bf16/fp16, 128 with a
 // block mask or for fp32), each wavefront 32 of its rows; K/V stream through
-// LDS in tiles of 64 keys (32 for fp32); QK^T and PV run on MFMA; the
+// LDS in tiles of 64 or 128 keys; QK^T and PV run on MFMA; the
 // online-softmax recurrence (running max, rescaled running sum, rescaled
 // accumulator, attention.cpp:628-673) lives in registers; the N x N score
 // matrix is never formed.
@@ -206,16 +206,22 @@ __device__ __forceinline__ float online_softmax_tile(const FwdArgs& a, f32x16 (&
 // ---------------------------------------------------------------------------
 // bf16 / fp16 inputs, fp32 accumulate: v_mfma_f32_32x32x16_{bf16,f16}.
 //
-// Every wavefront owns 32 query rows. K/V tiles of 64 keys are staged
-// global -> registers -> LDS one tile ahead. Loads are unconditional: rows
-// past the end are clamped to the last row, their V zeroed and their scores
+// Every wavefront owns 32 query rows. K/V tiles are staged one tile ahead:
+// global -> registers -> LDS in the D=64, score_mod and block-mask kernels;
+// by global_load_lds_dwordx4 copies straight into LDS (no staging registers,
+// no LDS store instructions) in the D=128 plain kernel, whose staged tile is
+// 128 keys computed in two 64-key steps. Loads are unconditional: rows past
+// the end are clamped to the last row, their V zeroed and their scores
 // masked, so no exec-masked branch breaks the compiler's wait counting.
 //
-// LDS layout: both tiles row-major [key][d] with padded row strides chosen
-// so that the K A-operand reads (ds_read_b128) and the V reads
-// (ds_read_b64_tr_b16, which deliver V^T fragments directly, so V is never
-// transposed in a separate pass) are free of bank conflicts, with every
-// per-read offset a compile-time immediate.
+// LDS layout: both tiles row-major [key][d]. Register-staged tiles use padded
+// row strides chosen so that the K A-operand reads (ds_read_b128) and the V
+// reads (ds_read_b64_tr_b16, which deliver V^T fragments directly, so V is
+// never transposed in a separate pass) are free of bank conflicts, with every
+// per-read offset a compile-time immediate. Copied tiles are unpadded (each
+// copy instruction writes 1 KB of consecutive LDS) and XOR-swizzle the
+// 16-byte chunks of a row instead, which keeps the same reads conflict-free
+// at one XOR per read.
 //
 // Workgroup schedule (every 16-bit call): lockstep. All wavefronts run S,
 // softmax and PV of a tile between two barriers; double-buffered LDS.
@@ -251,16 +257,31 @@ enum ScoreMod { MOD_PLAIN = 0, MOD_GENERAL = 1 };
 // them, i.e. the K/V prefetch) at each use.
 __device__ __forceinline__ void wait_vm_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-template <int D, int BN>
+// One 16-byte global -> LDS copy per lane (lane L writes lds + 16 L; lds is
+// wave-uniform). Written as assembly so that the compiler does not make LDS
+// reads of the other stage wait for it; completion is awaited explicitly
+// (wait_vm_loads) before the barrier that publishes the tile. M0 is restored.
+__device__ __forceinline__ void dma16(const void* g, unsigned lds) {
+    unsigned save;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(save) : "v"(g), "s"(lds) : "memory");
+}
+
+template <int D, int BN, bool SWZ = false>
 struct TileLayout {
     static constexpr int RB = D * 2;              // bytes of one K/V row
     static constexpr int CPR = D / 8;             // 16-byte chunks per row
+    // SWZ: unpadded rows written by global -> LDS copies; chunk c of row r at
+    // position c ^ kswz(r) (K) or c ^ vswz(r) (V), which keeps both read patterns
+    // conflict-free.
+    static __device__ __forceinline__ int kswz(int row) { return D == 128 ? (row & 15) : ((row >> 1) & 7); }
+    static __device__ __forceinline__ int vswz(int row) { return D == 128 ? 4 * (row & 3) : 4 * ((row >> 1) & 1); }
     // Row strides with padding. K: rows kappa(0..15) read at one chunk column
     // by 16 lanes land in 16 distinct 16-byte bank groups (stride/16 odd).
     // V: the transposed reads of rows {k..k+3} x 4 chunk columns land in 4
     // distinct groups of 4 (stride/16 = 4 mod 8 for D=128, 12 for D=64).
-    static constexpr int KSTR = RB + 16;
-    static constexpr int VSTR = RB + 64;
+    static constexpr int KSTR = SWZ ? RB : RB + 16;
+    static constexpr int VSTR = SWZ ? RB : RB + 64;
     static constexpr int KTILE = BN * KSTR;
     static constexpr int VTILE = BN * VSTR;
     static constexpr int STAGE = KTILE + VTILE;   // K tile then V tile
@@ -303,7 +324,8 @@ template <typename T, int D, int MOD, bool LIST, int NTHREADS, int BN_, int SB =
 struct Wave32 {
     using M16 = Mfma16<T>;
     using v8 = typename M16::v8;
-    using L = TileLayout<D, BN_ * SB>;
+    static constexpr bool DMA = SB > 1;  // K/V staged by global -> LDS copies
+    using L = TileLayout<D, BN_ * SB, DMA>;
     static constexpr int BN = BN_;
     static constexpr int SN = BN_ * SB;                 // keys per staged tile
     static constexpr int CPT = SN * L::CPR / NTHREADS;  // 16-byte chunks per thread per tile
@@ -332,6 +354,9 @@ struct Wave32 {
     int staged_kt;
     // LDS read lane offsets
     int k_lane_off, v_lane_off;
+    // DMA staging: lane offsets (elements) of its chunk in rows r0 + u*DSTEP
+    static constexpr int DSTEP = 64 * (NTHREADS / 64) / L::CPR;
+    int dma_row0, dma_koff, dma_voff;
 
     __device__ __forceinline__ Wave32(const FwdArgs& args, unsigned char* sm, int bh, int q0, int wv)
         : a(args), smem(sm), wave(wv) {
@@ -376,6 +401,21 @@ struct Wave32 {
         k_lane_off = kappa(r) * L::KSTR + 16 * g;
         const int v_dquad = 16 * (G & 1) + 4 * ((j & 1) * 2 + ((j >> 1) & 1));  // d offset within 32
         v_lane_off = L::KTILE + (8 * g + (j >> 2)) * L::VSTR + (v_dquad >> 3) * 16 + (v_dquad & 4) * 2;
+        if constexpr (DMA) {
+            static_assert(D == 128, "swizzled read addressing below assumes 256-byte rows");
+            // K chunk 2c+g of row kappa(r) sits at 32 (c ^ kh) + 16 gl: read at k_lane_off ^ 32c
+            const int ksw = L::kswz(kappa(r));
+            k_lane_off = kappa(r) * L::KSTR + 16 * ((g ^ ksw) & 1) + 32 * (ksw >> 1);
+            // V chunk (v_dquad>>3) + 4 db of row 8g + j/4 sits at chunk + 4 (db ^ rq): read at v_lane_off ^ 64 db
+            const int rq = L::vswz(8 * g + (j >> 2)) >> 2;
+            v_lane_off = L::KTILE + (8 * g + (j >> 2)) * L::VSTR + (v_dquad >> 3) * 16 + (v_dquad & 4) * 2 + 64 * rq;
+            // copies: wave instruction u covers 16-byte slots 64 (u NWAVES + wave) + lane
+            const int slot0 = 64 * wave + lane;
+            dma_row0 = slot0 / L::CPR;
+            const int pos = slot0 % L::CPR;
+            dma_koff = dma_row0 * (int)a.k_sn + 8 * (pos ^ L::kswz(dma_row0));
+            dma_voff = dma_row0 * (int)a.v_sn + 8 * (pos ^ L::vswz(dma_row0));
+        }
     }
 
     // Entry of tile step `it` (a global load with a list: issue it early).
@@ -427,6 +467,45 @@ struct Wave32 {
         }
     }
 
+    // Global -> LDS copy of staged tile kt into `stage_off` (asynchronous).
+    // Rows past N read row N-1; zero_tail clears their V rows once landed.
+    __device__ __forceinline__ void copy_tile(int kt, int stage_off) {
+        const int k0 = kt * SN;
+        const T* kt_base = Kp + (int64_t)k0 * a.k_sn;
+        const T* vt_base = Vp + (int64_t)k0 * a.v_sn;
+        const unsigned lds0 = (unsigned)(uintptr_t)smem + stage_off + 1024 * wave;
+        constexpr int NW = NTHREADS / 64;
+        if (k0 + SN <= a.N) {
+            const T* kp = kt_base + dma_koff;
+            const T* vp = vt_base + dma_voff;
+            const int64_t kstep = (int64_t)DSTEP * a.k_sn, vstep = (int64_t)DSTEP * a.v_sn;
+#pragma unroll
+            for (int u = 0; u < CPT; ++u) {
+                dma16(kp, lds0 + 1024 * NW * u);
+                dma16(vp, lds0 + L::KTILE + 1024 * NW * u);
+                kp += kstep;
+                vp += vstep;
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < CPT; ++u) {
+                const int row = min(k0 + dma_row0 + u * DSTEP, a.N - 1) - k0 - dma_row0;
+                dma16(kt_base + (int64_t)row * a.k_sn + dma_koff, lds0 + 1024 * NW * u);
+                dma16(vt_base + (int64_t)row * a.v_sn + dma_voff, lds0 + L::KTILE + 1024 * NW * u);
+            }
+        }
+    }
+    __device__ __forceinline__ void zero_tail(int kt, int stage_off) {
+        const int k0 = kt * SN;
+        if (k0 + SN <= a.N) return;
+        constexpr int NW = NTHREADS / 64;
+        const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int u = 0; u < CPT; ++u)
+            if (k0 + dma_row0 + u * DSTEP >= a.N)
+                *(u32x4*)(smem + stage_off + L::KTILE + 1024 * wave + 1024 * NW * u + 16 * (tid & 63)) = zero;
+    }
+
     // S^T = K Q^T for the tile in LDS stage `stage_off`. With a score_mod
     // (longer softmax) all K fragments are read before the first MFMA.
     __device__ __forceinline__ void qk(int stage_off, int sub = 0) {
@@ -450,8 +529,11 @@ struct Wave32 {
         // scheduling fences keep the compiler from sinking each read next to
         // its MFMA (it otherwise keeps two in flight).
         constexpr int NF = (BN / 32) * (D / 16);
+        const lds_u8* kbs = (const lds_u8*)smem + stage_off + sub * BN * L::KSTR;
         auto rd = [&](int i) {
             const int sb = i / (D / 16), c = i % (D / 16);
+            if constexpr (DMA)
+                return __builtin_bit_cast(v8, *(const lds_u32x4*)(kbs + 32 * sb * L::KSTR + (k_lane_off ^ (32 * c))));
             return __builtin_bit_cast(v8, *(const lds_u32x4*)(kb + 32 * sb * L::KSTR + 32 * c));
         };
         v8 f[kFragAhead];
@@ -473,7 +555,14 @@ struct Wave32 {
     // before the first MFMA.
     __device__ __forceinline__ void pv(int stage_off, int sub = 0) {
         const lds_u8* vb = (const lds_u8*)smem + stage_off + v_lane_off + sub * BN * L::VSTR;
+        const lds_u8* vbs = (const lds_u8*)smem + stage_off + sub * BN * L::VSTR;
         auto vfrag = [&](int c, int db) {
+            if constexpr (DMA) {
+                const int off = v_lane_off ^ (64 * db);
+                const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vbs + (16 * c) * L::VSTR + off));
+                const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vbs + (16 * c + 4) * L::VSTR + off));
+                return __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            }
             const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (lds_i16x4*)(vb + (16 * c) * L::VSTR + 64 * db));
             const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -747,18 +836,27 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
     W w(a, smem, bh, qt * BLOCK_M, wave);
     if constexpr (SB > 1) {
         // SB compute steps of BN keys per staged tile of SB*BN keys (one
-        // barrier per staged tile); plain scale without a list only.
-        static_assert(!LIST && MOD == MOD_PLAIN, "sub-steps: plain scale, no list");
+        // barrier per staged tile); plain scale without a list only. Tile
+        // st+1 is copied global -> LDS (no registers) into the free stage at
+        // the start of step st and awaited before the barrier that ends it.
+        static_assert(!LIST && MOD == MOD_PLAIN && W::DMA, "sub-steps: plain scale, no list, LDS copies");
         const int q0 = qt * BLOCK_M;
         const int kend = a.causal ? min(a.N, q0 + BLOCK_M) : a.N;
         const int nst = (kend + W::SN - 1) / W::SN;      // staged tiles
-        if (nst > 0) w.load_tile(0);
+        if (nst == 0) {  // uniform over the workgroup
+            w.store_output();
+            return;
+        }
+        // (returning early keeps every path into the loop through the wait
+        // below, so the compiler sees the Q fragments resident in the loop)
+        w.copy_tile(0, 0);
         wait_vm_loads();
-        if (nst > 0) w.store_tile(0);
-        if (nst > 1) w.load_tile(1);
+        w.zero_tail(0, 0);
         __syncthreads();
         for (int st = 0; st < nst; ++st) {
             const int stage = (st & 1) * L::STAGE;
+            const int nstage = ((st + 1) & 1) * L::STAGE;
+            if (st + 1 < nst) w.copy_tile(st + 1, nstage);
 #pragma unroll
             for (int j = 0; j < SB; ++j) {
                 const int e = st * SB + j;               // BN-key compute tile
@@ -772,8 +870,8 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
                     __builtin_amdgcn_s_setprio(0);
                 }
             }
-            if (st + 1 < nst) w.store_tile(((st + 1) & 1) * L::STAGE);
-            if (st + 2 < nst) w.load_tile(st + 2);
+            wait_vm_loads();
+            if (st + 1 < nst) w.zero_tail(st + 1, nstage);
             __syncthreads();
         }
         w.store_output();
@@ -817,7 +915,7 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
 
 template <typename T, int D, int MOD, bool LIST, int NWAVES, bool PAIRED, int BN = kBlockN16, int SB = 1>
 __global__ __launch_bounds__(NWAVES * 64, 8 / NWAVES) void flash_fwd_lockstep_kernel(FwdArgs a) {
-    using L = TileLayout<D, BN * SB>;
+    using L = TileLayout<D, BN * SB, (SB > 1)>;
     __shared__ __attribute__((aligned(16))) unsigned char smem[2 * L::STAGE];
     int bh, qts[2];
     const int n = work_tiles(a, PAIRED, bh, qts);
