@@ -207,10 +207,10 @@ __device__ __forceinline__ float online_softmax_tile(const FwdArgs& a, f32x16 (&
 // bf16 / fp16 inputs, fp32 accumulate: v_mfma_f32_32x32x16_{bf16,f16}.
 //
 // Every wavefront owns 32 query rows. K/V tiles are staged one tile ahead:
-// global -> registers -> LDS in the D=64, score_mod and block-mask kernels;
+// global -> registers -> LDS in the score_mod and block-mask kernels;
 // by global_load_lds_dwordx4 copies straight into LDS (no staging registers,
-// no LDS store instructions) in the D=128 plain kernel, whose staged tile is
-// 128 keys computed in two 64-key steps. Loads are unconditional: rows past
+// no LDS store instructions) in the plain-scale kernels without a block mask,
+// whose staged tile is 128 keys (computed in two 64-key steps at D=128). Loads are unconditional: rows past
 // the end are clamped to the last row, their V zeroed and their scores
 // masked, so no exec-masked branch breaks the compiler's wait counting.
 //
@@ -324,7 +324,7 @@ template <typename T, int D, int MOD, bool LIST, int NTHREADS, int BN_, int SB =
 struct Wave32 {
     using M16 = Mfma16<T>;
     using v8 = typename M16::v8;
-    static constexpr bool DMA = SB > 1;  // K/V staged by global -> LDS copies
+    static constexpr bool DMA = SB > 1 || (D == 64 && MOD == MOD_PLAIN && !LIST);  // K/V staged by global -> LDS copies
     using L = TileLayout<D, BN_ * SB, DMA>;
     static constexpr int BN = BN_;
     static constexpr int SN = BN_ * SB;                 // keys per staged tile
@@ -402,7 +402,6 @@ struct Wave32 {
         const int v_dquad = 16 * (G & 1) + 4 * ((j & 1) * 2 + ((j >> 1) & 1));  // d offset within 32
         v_lane_off = L::KTILE + (8 * g + (j >> 2)) * L::VSTR + (v_dquad >> 3) * 16 + (v_dquad & 4) * 2;
         if constexpr (DMA) {
-            static_assert(D == 128, "swizzled read addressing below assumes 256-byte rows");
             // K chunk 2c+g of row kappa(r) sits at 32 (c ^ kh) + 16 gl: read at k_lane_off ^ 32c
             const int ksw = L::kswz(kappa(r));
             k_lane_off = kappa(r) * L::KSTR + 16 * ((g ^ ksw) & 1) + 32 * (ksw >> 1);
@@ -834,12 +833,12 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
     using L = typename W::L;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     W w(a, smem, bh, qt * BLOCK_M, wave);
-    if constexpr (SB > 1) {
+    if constexpr (W::DMA) {
         // SB compute steps of BN keys per staged tile of SB*BN keys (one
-        // barrier per staged tile); plain scale without a list only. Tile
+        // barrier per staged tile); plain scale without a list. Tile
         // st+1 is copied global -> LDS (no registers) into the free stage at
         // the start of step st and awaited before the barrier that ends it.
-        static_assert(!LIST && MOD == MOD_PLAIN && W::DMA, "sub-steps: plain scale, no list, LDS copies");
+        static_assert(!LIST && MOD == MOD_PLAIN, "LDS copies: plain scale, no list");
         const int q0 = qt * BLOCK_M;
         const int kend = a.causal ? min(a.N, q0 + BLOCK_M) : a.N;
         const int nst = (kend + W::SN - 1) / W::SN;      // staged tiles
@@ -915,7 +914,7 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
 
 template <typename T, int D, int MOD, bool LIST, int NWAVES, bool PAIRED, int BN = kBlockN16, int SB = 1>
 __global__ __launch_bounds__(NWAVES * 64, 8 / NWAVES) void flash_fwd_lockstep_kernel(FwdArgs a) {
-    using L = TileLayout<D, BN * SB, (SB > 1)>;
+    using L = TileLayout<D, BN * SB, (SB > 1 || (D == 64 && MOD == MOD_PLAIN && !LIST))>;
     __shared__ __attribute__((aligned(16))) unsigned char smem[2 * L::STAGE];
     int bh, qts[2];
     const int n = work_tiles(a, PAIRED, bh, qts);
