@@ -207,10 +207,11 @@ __device__ __forceinline__ float online_softmax_tile(const FwdArgs& a, f32x16 (&
 // bf16 / fp16 inputs, fp32 accumulate: v_mfma_f32_32x32x16_{bf16,f16}.
 //
 // Every wavefront owns 32 query rows. K/V tiles are staged one tile ahead:
-// global -> registers -> LDS in the score_mod and block-mask kernels;
+// global -> registers -> LDS in the block-mask and D=64 score_mod kernels;
 // by global_load_lds_dwordx4 copies straight into LDS (no staging registers,
-// no LDS store instructions) in the plain-scale kernels without a block mask,
-// whose staged tile is 128 keys (computed in two 64-key steps at D=128). Loads are unconditional: rows past
+// no LDS store instructions) in the kernels without a block mask (the D=64
+// score_mod kernel aside); the plain-scale staged tile is 128 keys (two
+// 64-key compute steps at D=128), the score_mod one 64. Loads are unconditional: rows past
 // the end are clamped to the last row, their V zeroed and their scores
 // masked, so no exec-masked branch breaks the compiler's wait counting.
 //
@@ -324,7 +325,9 @@ template <typename T, int D, int MOD, bool LIST, int NTHREADS, int BN_, int SB =
 struct Wave32 {
     using M16 = Mfma16<T>;
     using v8 = typename M16::v8;
-    static constexpr bool DMA = SB > 1 || (D == 64 && MOD == MOD_PLAIN && !LIST);  // K/V staged by global -> LDS copies
+    // K/V staged by global -> LDS copies: every kernel without a block-mask
+    // list except the D=64 score_mod one (register staging there)
+    static constexpr bool DMA = !LIST && (MOD == MOD_PLAIN || D == 128);
     using L = TileLayout<D, BN_ * SB, DMA>;
     static constexpr int BN = BN_;
     static constexpr int SN = BN_ * SB;                 // keys per staged tile
@@ -505,11 +508,12 @@ struct Wave32 {
                 *(u32x4*)(smem + stage_off + L::KTILE + 1024 * wave + 1024 * NW * u + 16 * (tid & 63)) = zero;
     }
 
-    // S^T = K Q^T for the tile in LDS stage `stage_off`. With a score_mod
-    // (longer softmax) all K fragments are read before the first MFMA.
+    // S^T = K Q^T for the tile in LDS stage `stage_off`. In the
+    // register-staged score_mod kernel (longer softmax) all K fragments are
+    // read before the first MFMA; elsewhere they run kFragAhead ahead.
     __device__ __forceinline__ void qk(int stage_off, int sub = 0) {
         const lds_u8* kb = (const lds_u8*)smem + stage_off + k_lane_off + sub * BN * L::KSTR;
-        if (MOD == MOD_GENERAL) {
+        if (MOD == MOD_GENERAL && !DMA) {
             v8 kf[BN / 32][D / 16];
 #pragma unroll
             for (int c = 0; c < D / 16; ++c)
@@ -550,8 +554,8 @@ struct Wave32 {
     }
 
     // O^T += V^T P^T for the tile in LDS stage `stage_off` (A operand from two
-    // transposed 4-key reads). With a score_mod all V^T fragments are read
-    // before the first MFMA.
+    // transposed 4-key reads). In the register-staged score_mod kernel all
+    // V^T fragments are read before the first MFMA.
     __device__ __forceinline__ void pv(int stage_off, int sub = 0) {
         const lds_u8* vb = (const lds_u8*)smem + stage_off + v_lane_off + sub * BN * L::VSTR;
         const lds_u8* vbs = (const lds_u8*)smem + stage_off + sub * BN * L::VSTR;
@@ -568,7 +572,7 @@ struct Wave32 {
                 (lds_i16x4*)(vb + (16 * c + 4) * L::VSTR + 64 * db));
             return __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         };
-        if (MOD == MOD_GENERAL) {
+        if (MOD == MOD_GENERAL && !DMA) {
             v8 vf[D / 32][BN / 16];
 #pragma unroll
             for (int c = 0; c < BN / 16; ++c)
@@ -835,10 +839,10 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
     W w(a, smem, bh, qt * BLOCK_M, wave);
     if constexpr (W::DMA) {
         // SB compute steps of BN keys per staged tile of SB*BN keys (one
-        // barrier per staged tile); plain scale without a list. Tile
+        // barrier per staged tile); no list. Tile
         // st+1 is copied global -> LDS (no registers) into the free stage at
         // the start of step st and awaited before the barrier that ends it.
-        static_assert(!LIST && MOD == MOD_PLAIN, "LDS copies: plain scale, no list");
+        static_assert(!LIST, "LDS copies: no list");
         const int q0 = qt * BLOCK_M;
         const int kend = a.causal ? min(a.N, q0 + BLOCK_M) : a.N;
         const int nst = (kend + W::SN - 1) / W::SN;      // staged tiles
@@ -860,13 +864,13 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
             for (int j = 0; j < SB; ++j) {
                 const int e = st * SB + j;               // BN-key compute tile
                 if (e * BN < kend && w.tile_active(e)) {
-                    __builtin_amdgcn_s_setprio(1);
+                    if (MOD == MOD_PLAIN) __builtin_amdgcn_s_setprio(1);
                     w.qk(stage, j);
-                    __builtin_amdgcn_s_setprio(0);
+                    if (MOD == MOD_PLAIN) __builtin_amdgcn_s_setprio(0);
                     w.softmax(e);
-                    __builtin_amdgcn_s_setprio(1);
+                    if (MOD == MOD_PLAIN) __builtin_amdgcn_s_setprio(1);
                     w.pv(stage, j);
-                    __builtin_amdgcn_s_setprio(0);
+                    if (MOD == MOD_PLAIN) __builtin_amdgcn_s_setprio(0);
                 }
             }
             wait_vm_loads();
@@ -914,7 +918,7 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
 
 template <typename T, int D, int MOD, bool LIST, int NWAVES, bool PAIRED, int BN = kBlockN16, int SB = 1>
 __global__ __launch_bounds__(NWAVES * 64, 8 / NWAVES) void flash_fwd_lockstep_kernel(FwdArgs a) {
-    using L = TileLayout<D, BN * SB, (SB > 1 || (D == 64 && MOD == MOD_PLAIN && !LIST))>;
+    using L = TileLayout<D, BN * SB, (!LIST && (MOD == MOD_PLAIN || D == 128))>;
     __shared__ __attribute__((aligned(16))) unsigned char smem[2 * L::STAGE];
     int bh, qts[2];
     const int n = work_tiles(a, PAIRED, bh, qts);
