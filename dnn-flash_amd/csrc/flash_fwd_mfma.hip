@@ -207,11 +207,11 @@ __device__ __forceinline__ float online_softmax_tile(const FwdArgs& a, f32x16 (&
 // bf16 / fp16 inputs, fp32 accumulate: v_mfma_f32_32x32x16_{bf16,f16}.
 //
 // Every wavefront owns 32 query rows. K/V tiles are staged one tile ahead:
-// global -> registers -> LDS in the block-mask and D=64 score_mod kernels;
+// global -> registers -> LDS in the block-mask kernels;
 // by global_load_lds_dwordx4 copies straight into LDS (no staging registers,
-// no LDS store instructions) in the kernels without a block mask (the D=64
-// score_mod kernel aside); the plain-scale staged tile is 128 keys (two
-// 64-key compute steps at D=128), the score_mod one 64. Loads are unconditional: rows past
+// no LDS store instructions) in the kernels without a block mask; the
+// plain-scale staged tile is 128 keys (two 64-key compute steps at D=128),
+// the score_mod one 64. Loads are unconditional: rows past
 // the end are clamped to the last row, their V zeroed and their scores
 // masked, so no exec-masked branch breaks the compiler's wait counting.
 //
@@ -325,9 +325,9 @@ template <typename T, int D, int MOD, bool LIST, int NTHREADS, int BN_, int SB =
 struct Wave32 {
     using M16 = Mfma16<T>;
     using v8 = typename M16::v8;
-    // K/V staged by global -> LDS copies: every kernel without a block-mask
-    // list except the D=64 score_mod one (register staging there)
-    static constexpr bool DMA = !LIST && (MOD == MOD_PLAIN || D == 128);
+    // K/V staged by global -> LDS copies in every kernel without a block-mask
+    // list (register staging with one)
+    static constexpr bool DMA = !LIST;
     using L = TileLayout<D, BN_ * SB, DMA>;
     static constexpr int BN = BN_;
     static constexpr int SN = BN_ * SB;                 // keys per staged tile
@@ -508,9 +508,9 @@ struct Wave32 {
                 *(u32x4*)(smem + stage_off + L::KTILE + 1024 * wave + 1024 * NW * u + 16 * (tid & 63)) = zero;
     }
 
-    // S^T = K Q^T for the tile in LDS stage `stage_off`. In the
-    // register-staged score_mod kernel (longer softmax) all K fragments are
-    // read before the first MFMA; elsewhere they run kFragAhead ahead.
+    // S^T = K Q^T for the tile in LDS stage `stage_off`. In the block-mask
+    // score_mod kernel (longer softmax) all K fragments are read before the
+    // first MFMA; elsewhere they run kFragAhead ahead.
     __device__ __forceinline__ void qk(int stage_off, int sub = 0) {
         const lds_u8* kb = (const lds_u8*)smem + stage_off + k_lane_off + sub * BN * L::KSTR;
         if (MOD == MOD_GENERAL && !DMA) {
@@ -554,8 +554,8 @@ struct Wave32 {
     }
 
     // O^T += V^T P^T for the tile in LDS stage `stage_off` (A operand from two
-    // transposed 4-key reads). In the register-staged score_mod kernel all
-    // V^T fragments are read before the first MFMA.
+    // transposed 4-key reads). In the block-mask score_mod kernel all V^T
+    // fragments are read before the first MFMA.
     __device__ __forceinline__ void pv(int stage_off, int sub = 0) {
         const lds_u8* vb = (const lds_u8*)smem + stage_off + v_lane_off + sub * BN * L::VSTR;
         const lds_u8* vbs = (const lds_u8*)smem + stage_off + sub * BN * L::VSTR;
@@ -918,7 +918,7 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
 
 template <typename T, int D, int MOD, bool LIST, int NWAVES, bool PAIRED, int BN = kBlockN16, int SB = 1>
 __global__ __launch_bounds__(NWAVES * 64, 8 / NWAVES) void flash_fwd_lockstep_kernel(FwdArgs a) {
-    using L = TileLayout<D, BN * SB, (!LIST && (MOD == MOD_PLAIN || D == 128))>;
+    using L = TileLayout<D, BN * SB, !LIST>;
     __shared__ __attribute__((aligned(16))) unsigned char smem[2 * L::STAGE];
     int bh, qts[2];
     const int n = work_tiles(a, PAIRED, bh, qts);
