@@ -206,23 +206,19 @@ __device__ __forceinline__ float online_softmax_tile(const FwdArgs& a, f32x16 (&
 // ---------------------------------------------------------------------------
 // bf16 / fp16 inputs, fp32 accumulate: v_mfma_f32_32x32x16_{bf16,f16}.
 //
-// Every wavefront owns 32 query rows. K/V tiles are staged one tile ahead:
-// global -> registers -> LDS in the block-mask kernels;
+// Every wavefront owns 32 query rows. K/V tiles are staged one tile ahead
 // by global_load_lds_dwordx4 copies straight into LDS (no staging registers,
-// no LDS store instructions) in the kernels without a block mask; the
-// plain-scale staged tile is 128 keys (two 64-key compute steps at D=128),
-// the score_mod one 64. Loads are unconditional: rows past
-// the end are clamped to the last row, their V zeroed and their scores
-// masked, so no exec-masked branch breaks the compiler's wait counting.
+// no LDS store instructions). With the plain scale and no block mask a
+// staged tile is 128 keys (two 64-key compute steps at D=128), otherwise 64.
+// Loads are unconditional: rows past the end are clamped to the last row,
+// their V zeroed and their scores masked, so no exec-masked branch breaks
+// the compiler's wait counting.
 //
-// LDS layout: both tiles row-major [key][d]. Register-staged tiles use padded
-// row strides chosen so that the K A-operand reads (ds_read_b128) and the V
-// reads (ds_read_b64_tr_b16, which deliver V^T fragments directly, so V is
-// never transposed in a separate pass) are free of bank conflicts, with every
-// per-read offset a compile-time immediate. Copied tiles are unpadded (each
-// copy instruction writes 1 KB of consecutive LDS) and XOR-swizzle the
-// 16-byte chunks of a row instead, which keeps the same reads conflict-free
-// at one XOR per read.
+// LDS layout (TileLayout): both tiles row-major [key][d], unpadded, with the
+// 16-byte chunks of a row XOR-swizzled so that the K A-operand reads
+// (ds_read_b128) and the V reads (ds_read_b64_tr_b16, which deliver V^T
+// fragments directly, so V is never transposed in a separate pass) are free
+// of bank conflicts at one XOR per read.
 //
 // Workgroup schedule (every 16-bit call): lockstep. All wavefronts run S,
 // softmax and PV of a tile between two barriers; double-buffered LDS.
@@ -268,26 +264,24 @@ __device__ __forceinline__ void dma16(const void* g, unsigned lds) {
                  : "=&s"(save) : "v"(g), "s"(lds) : "memory");
 }
 
-template <int D, int BN, bool SWZ = false>
+// K and V tiles in LDS: row-major [key][d], unpadded (each global -> LDS
+// copy instruction writes 1 KB of consecutive LDS). Chunk c (16 bytes) of row
+// r sits at position c ^ kswz(r) (K) or c ^ vswz(r) (V), which keeps both
+// read patterns free of bank conflicts (measured with SQ_LDS_BANK_CONFLICT):
+// K fragments read rows kappa(0..15) at one chunk per 16 lanes; V^T fragments
+// are transposing reads of 4 rows x 2 chunks per 16 lanes. For D = 64 two rows
+// share a 256-byte bank line, hence row >> 1.
+template <int D, int BN>
 struct TileLayout {
     static constexpr int RB = D * 2;              // bytes of one K/V row
     static constexpr int CPR = D / 8;             // 16-byte chunks per row
-    // SWZ: unpadded rows written by global -> LDS copies; chunk c of row r at
-    // position c ^ kswz(r) (K) or c ^ vswz(r) (V), which keeps both read patterns
-    // conflict-free.
     static __device__ __forceinline__ int kswz(int row) { return D == 128 ? (row & 15) : ((row >> 1) & 7); }
     static __device__ __forceinline__ int vswz(int row) { return D == 128 ? 4 * (row & 3) : 4 * ((row >> 1) & 1); }
-    // Row strides with padding. K: rows kappa(0..15) read at one chunk column
-    // by 16 lanes land in 16 distinct 16-byte bank groups (stride/16 odd).
-    // V: the transposed reads of rows {k..k+3} x 4 chunk columns land in 4
-    // distinct groups of 4 (stride/16 = 4 mod 8 for D=128, 12 for D=64).
-    static constexpr int KSTR = SWZ ? RB : RB + 16;
-    static constexpr int VSTR = SWZ ? RB : RB + 64;
+    static constexpr int KSTR = RB;
+    static constexpr int VSTR = RB;
     static constexpr int KTILE = BN * KSTR;
     static constexpr int VTILE = BN * VSTR;
     static constexpr int STAGE = KTILE + VTILE;   // K tile then V tile
-    static __device__ __forceinline__ int kaddr(int row, int chunk) { return row * KSTR + (chunk << 4); }
-    static __device__ __forceinline__ int vaddr(int row, int chunk) { return row * VSTR + (chunk << 4); }
 };
 
 // max over both 32-lane halves (lane l and l^32 hold the same query row)
@@ -327,12 +321,10 @@ struct Wave32 {
     using v8 = typename M16::v8;
     // K/V staged by global -> LDS copies in every kernel without a block-mask
     // list (register staging with one)
-    static constexpr bool DMA = !LIST;
-    using L = TileLayout<D, BN_ * SB, DMA>;
+    using L = TileLayout<D, BN_ * SB>;
     static constexpr int BN = BN_;
     static constexpr int SN = BN_ * SB;                 // keys per staged tile
     static constexpr int CPT = SN * L::CPR / NTHREADS;  // 16-byte chunks per thread per tile
-    static constexpr int RSTEP = NTHREADS / L::CPR;      // rows between a thread's chunks
     static_assert(CPT >= 1 && SN * L::CPR % NTHREADS == 0 && NTHREADS % L::CPR == 0,
                   "tile must split evenly");
 
@@ -351,13 +343,9 @@ struct Wave32 {
     float m_run, l_run;
     float slope;
     const float* bias_row;
-    // staging: chunk u of this thread is row ld_row + u*RSTEP, 16-byte column ld_col
-    int ld_row, ld_koff, ld_voff, st_koff;
-    u32x4 kreg[CPT], vreg[CPT];
-    int staged_kt;
     // LDS read lane offsets
     int k_lane_off, v_lane_off;
-    // DMA staging: lane offsets (elements) of its chunk in rows r0 + u*DSTEP
+    // K/V copies: lane offsets (elements) of its chunk in rows dma_row0 + u*DSTEP
     static constexpr int DSTEP = 64 * (NTHREADS / 64) / L::CPR;
     int dma_row0, dma_koff, dma_voff;
 
@@ -390,34 +378,24 @@ struct Wave32 {
             if (a.bias_kind == BIAS_DENSE)
                 bias_row = a.bias + b * a.bias_sb + h * a.bias_sh + (int64_t)min(my_q, a.M - 1) * a.bias_sm;
         }
-        ld_row = tid / L::CPR;
-        const int ld_col = tid % L::CPR;
-        ld_koff = ld_row * (int)a.k_sn + 8 * ld_col;
-        ld_voff = ld_row * (int)a.v_sn + 8 * ld_col;
-        st_koff = L::kaddr(ld_row, ld_col);
-        staged_kt = 0;
         // K: A-operand row kappa(r) of a 32-key block, chunk 2c+g. V (transposed
         // reads): input lane j of a 16-lane group reads key (j/4) of a 4-key
         // group at d-chunk cmap(j%4) of the group's 16 columns; cmap = {0,2,1,3}
         // applies kappa to the output rows.
         const int G = lane >> 4, j = lane & 15;
-        k_lane_off = kappa(r) * L::KSTR + 16 * g;
         const int v_dquad = 16 * (G & 1) + 4 * ((j & 1) * 2 + ((j >> 1) & 1));  // d offset within 32
-        v_lane_off = L::KTILE + (8 * g + (j >> 2)) * L::VSTR + (v_dquad >> 3) * 16 + (v_dquad & 4) * 2;
-        if constexpr (DMA) {
-            // K chunk 2c+g of row kappa(r) sits at 32 (c ^ kh) + 16 gl: read at k_lane_off ^ 32c
-            const int ksw = L::kswz(kappa(r));
-            k_lane_off = kappa(r) * L::KSTR + 16 * ((g ^ ksw) & 1) + 32 * (ksw >> 1);
-            // V chunk (v_dquad>>3) + 4 db of row 8g + j/4 sits at chunk + 4 (db ^ rq): read at v_lane_off ^ 64 db
-            const int rq = L::vswz(8 * g + (j >> 2)) >> 2;
-            v_lane_off = L::KTILE + (8 * g + (j >> 2)) * L::VSTR + (v_dquad >> 3) * 16 + (v_dquad & 4) * 2 + 64 * rq;
-            // copies: wave instruction u covers 16-byte slots 64 (u NWAVES + wave) + lane
-            const int slot0 = 64 * wave + lane;
-            dma_row0 = slot0 / L::CPR;
-            const int pos = slot0 % L::CPR;
-            dma_koff = dma_row0 * (int)a.k_sn + 8 * (pos ^ L::kswz(dma_row0));
-            dma_voff = dma_row0 * (int)a.v_sn + 8 * (pos ^ L::vswz(dma_row0));
-        }
+        // K chunk 2c+g of row kappa(r) sits at 32 (c ^ kh) + 16 gl: read at k_lane_off ^ 32c
+        const int ksw = L::kswz(kappa(r));
+        k_lane_off = kappa(r) * L::KSTR + 16 * ((g ^ ksw) & 1) + 32 * (ksw >> 1);
+        // V chunk (v_dquad>>3) + 4 db of row 8g + j/4 sits at chunk + 4 (db ^ rq): read at v_lane_off ^ 64 db
+        const int rq = L::vswz(8 * g + (j >> 2)) >> 2;
+        v_lane_off = L::KTILE + (8 * g + (j >> 2)) * L::VSTR + (v_dquad >> 3) * 16 + (v_dquad & 4) * 2 + 64 * rq;
+        // copies: wave instruction u covers 16-byte slots 64 (u NWAVES + wave) + lane
+        const int slot0 = 64 * wave + lane;
+        dma_row0 = slot0 / L::CPR;
+        const int pos = slot0 % L::CPR;
+        dma_koff = dma_row0 * (int)a.k_sn + 8 * (pos ^ L::kswz(dma_row0));
+        dma_voff = dma_row0 * (int)a.v_sn + 8 * (pos ^ L::vswz(dma_row0));
     }
 
     // Entry of tile step `it` (a global load with a list: issue it early).
@@ -430,43 +408,6 @@ struct Wave32 {
     // causal diagonal or ragged end inside the tile
     __device__ __forceinline__ bool tile_crosses(int kt) const {
         return (kt * BN + BN > a.N) || (a.causal && kt * BN + BN - 1 > qw0);
-    }
-
-    // Global -> register staging of this thread's share of one K/V tile: a
-    // uniform tile base plus fixed 32-bit lane offsets; in the last, ragged
-    // tile rows past N are clamped to N-1.
-    __device__ __forceinline__ void load_tile(int kt) {
-        const int k0 = kt * SN;
-        staged_kt = kt;
-        const T* kt_base = Kp + (int64_t)k0 * a.k_sn;
-        const T* vt_base = Vp + (int64_t)k0 * a.v_sn;
-        if (k0 + SN <= a.N) {
-#pragma unroll
-            for (int u = 0; u < CPT; ++u) {
-                kreg[u] = *(const u32x4*)(kt_base + (int64_t)u * RSTEP * a.k_sn + ld_koff);
-                vreg[u] = *(const u32x4*)(vt_base + (int64_t)u * RSTEP * a.v_sn + ld_voff);
-            }
-        } else {
-#pragma unroll
-            for (int u = 0; u < CPT; ++u) {
-                // rows past N read row N-1 (their V is zeroed in LDS, their scores masked)
-                const int row = min(k0 + ld_row + u * RSTEP, a.N - 1) - k0 - ld_row;
-                kreg[u] = *(const u32x4*)(kt_base + (int64_t)row * a.k_sn + ld_koff);
-                vreg[u] = *(const u32x4*)(vt_base + (int64_t)row * a.v_sn + ld_voff);
-            }
-        }
-    }
-    __device__ __forceinline__ void store_tile(int stage_off) {
-        unsigned char* base = smem + stage_off;
-        const int k0 = staged_kt * SN;
-        // V chunk of the same (row, column): after the K tile, with the V row stride
-        const int st_voff = st_koff + L::KTILE + ld_row * (L::VSTR - L::KSTR);
-#pragma unroll
-        for (int u = 0; u < CPT; ++u) {
-            *(u32x4*)(base + st_koff + u * RSTEP * L::KSTR) = kreg[u];
-            const u32x4 zero = {0u, 0u, 0u, 0u};
-            *(u32x4*)(base + st_voff + u * RSTEP * L::VSTR) = (k0 + ld_row + u * RSTEP < a.N) ? vreg[u] : zero;
-        }
     }
 
     // Global -> LDS copy of staged tile kt into `stage_off` (asynchronous).
@@ -508,26 +449,8 @@ struct Wave32 {
                 *(u32x4*)(smem + stage_off + L::KTILE + 1024 * wave + 1024 * NW * u + 16 * (tid & 63)) = zero;
     }
 
-    // S^T = K Q^T for the tile in LDS stage `stage_off`. In the block-mask
-    // score_mod kernel (longer softmax) all K fragments are read before the
-    // first MFMA; elsewhere they run kFragAhead ahead.
+    // S^T = K Q^T for the tile in LDS stage `stage_off`.
     __device__ __forceinline__ void qk(int stage_off, int sub = 0) {
-        const lds_u8* kb = (const lds_u8*)smem + stage_off + k_lane_off + sub * BN * L::KSTR;
-        if (MOD == MOD_GENERAL && !DMA) {
-            v8 kf[BN / 32][D / 16];
-#pragma unroll
-            for (int c = 0; c < D / 16; ++c)
-#pragma unroll
-                for (int sb = 0; sb < BN / 32; ++sb)
-                    kf[sb][c] = __builtin_bit_cast(v8, *(const lds_u32x4*)(kb + 32 * sb * L::KSTR + 32 * c));
-#pragma unroll
-            for (int sb = 0; sb < BN / 32; ++sb) s[sb] = f32x16{};
-#pragma unroll
-            for (int c = 0; c < D / 16; ++c)
-#pragma unroll
-                for (int sb = 0; sb < BN / 32; ++sb) s[sb] = M16::mma(kf[sb][c], qf[c], s[sb]);
-            return;
-        }
         // Fragments are read kFragAhead MFMAs ahead of their use; the
         // scheduling fences keep the compiler from sinking each read next to
         // its MFMA (it otherwise keeps two in flight).
@@ -535,9 +458,7 @@ struct Wave32 {
         const lds_u8* kbs = (const lds_u8*)smem + stage_off + sub * BN * L::KSTR;
         auto rd = [&](int i) {
             const int sb = i / (D / 16), c = i % (D / 16);
-            if constexpr (DMA)
-                return __builtin_bit_cast(v8, *(const lds_u32x4*)(kbs + 32 * sb * L::KSTR + (k_lane_off ^ (32 * c))));
-            return __builtin_bit_cast(v8, *(const lds_u32x4*)(kb + 32 * sb * L::KSTR + 32 * c));
+            return __builtin_bit_cast(v8, *(const lds_u32x4*)(kbs + 32 * sb * L::KSTR + (k_lane_off ^ (32 * c))));
         };
         v8 f[kFragAhead];
 #pragma unroll
@@ -554,36 +475,15 @@ struct Wave32 {
     }
 
     // O^T += V^T P^T for the tile in LDS stage `stage_off` (A operand from two
-    // transposed 4-key reads). In the block-mask score_mod kernel all V^T
-    // fragments are read before the first MFMA.
+    // transposed 4-key reads).
     __device__ __forceinline__ void pv(int stage_off, int sub = 0) {
-        const lds_u8* vb = (const lds_u8*)smem + stage_off + v_lane_off + sub * BN * L::VSTR;
         const lds_u8* vbs = (const lds_u8*)smem + stage_off + sub * BN * L::VSTR;
         auto vfrag = [&](int c, int db) {
-            if constexpr (DMA) {
-                const int off = v_lane_off ^ (64 * db);
-                const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vbs + (16 * c) * L::VSTR + off));
-                const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vbs + (16 * c + 4) * L::VSTR + off));
-                return __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-            }
-            const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_i16x4*)(vb + (16 * c) * L::VSTR + 64 * db));
-            const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_i16x4*)(vb + (16 * c + 4) * L::VSTR + 64 * db));
+            const int off = v_lane_off ^ (64 * db);
+            const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vbs + (16 * c) * L::VSTR + off));
+            const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vbs + (16 * c + 4) * L::VSTR + off));
             return __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         };
-        if (MOD == MOD_GENERAL && !DMA) {
-            v8 vf[D / 32][BN / 16];
-#pragma unroll
-            for (int c = 0; c < BN / 16; ++c)
-#pragma unroll
-                for (int db = 0; db < D / 32; ++db) vf[db][c] = vfrag(c, db);
-#pragma unroll
-            for (int c = 0; c < BN / 16; ++c)
-#pragma unroll
-                for (int db = 0; db < D / 32; ++db) o[db] = M16::mma(vf[db][c], pf[c], o[db]);
-            return;
-        }
         // V^T fragments kFragAhead MFMAs ahead (see qk)
         constexpr int NF = (D / 32) * (BN / 16);
         v8 f[kFragAhead];
@@ -824,10 +724,10 @@ __device__ __forceinline__ void tile_range(const FwdArgs& a, int qt, int block_m
 }
 
 // All wavefronts run S, softmax and PV of a tile step between two barriers;
-// double-buffered LDS. Tile it+1 is stored to LDS at the end of step it, and
-// tile it+2 is loaded into registers right after, so its global latency is
-// hidden behind a whole step. With a list, entries are loaded three steps
-// ahead of their use.
+// double-buffered LDS. The copies of tile it+1 go into the free stage at the
+// start of step it and are awaited before the barrier that ends it, so their
+// latency hides behind a whole step. With a list, entries are loaded two
+// steps ahead of their use.
 template <typename T, int D, int MOD, bool LIST, int NWAVES, int BN, int SB = 1>
 __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* smem, int bh, int qt) {
     constexpr int NTHREADS = NWAVES * 64;
@@ -837,7 +737,7 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
     using L = typename W::L;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     W w(a, smem, bh, qt * BLOCK_M, wave);
-    if constexpr (W::DMA) {
+    if constexpr (!LIST) {
         // SB compute steps of BN keys per staged tile of SB*BN keys (one
         // barrier per staged tile); no list. Tile
         // st+1 is copied global -> LDS (no registers) into the free stage at
@@ -864,6 +764,11 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
             for (int j = 0; j < SB; ++j) {
                 const int e = st * SB + j;               // BN-key compute tile
                 if (e * BN < kend && w.tile_active(e)) {
+                    // Plain scale: matrix phases at wave priority 1 and the
+                    // softmax at 0, so that a wavefront ready for MFMAs issues
+                    // first when the two wavefronts of a SIMD drift apart
+                    // (measured +1-2 %; with a score_mod the longer softmax is
+                    // better left at equal priority).
                     if (MOD == MOD_PLAIN) __builtin_amdgcn_s_setprio(1);
                     w.qk(stage, j);
                     if (MOD == MOD_PLAIN) __builtin_amdgcn_s_setprio(0);
@@ -882,22 +787,23 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
     }
     tile_range(a, qt, BLOCK_M, BN, w.ntiles, w.list);
     const int ntiles = w.ntiles;
-
-    int e_cur = ntiles > 0 ? w.entry(0) : 0;
+    // entry it+1 is copied during step it
+    if (ntiles == 0) {
+        w.store_output();
+        return;
+    }
+    int e_cur = w.entry(0);
     int e_nxt = ntiles > 1 ? w.entry(1) : 0;
-    if (ntiles > 0) w.load_tile(w.tile_of(e_cur));
+    w.copy_tile(w.tile_of(e_cur), 0);
     wait_vm_loads();
-    if (ntiles > 0) w.store_tile(0);
-    if (ntiles > 1) w.load_tile(w.tile_of(e_nxt));
-    int e_nn = ntiles > 2 ? w.entry(2) : 0;
+    w.zero_tail(w.tile_of(e_cur), 0);
     __syncthreads();
     for (int it = 0; it < ntiles; ++it) {
         const int stage = (it & 1) * L::STAGE;
+        const int nstage = ((it + 1) & 1) * L::STAGE;
+        if (it + 1 < ntiles) w.copy_tile(w.tile_of(e_nxt), nstage);
+        const int e_nn = it + 2 < ntiles ? w.entry(it + 2) : 0;
         if (w.tile_active(e_cur)) {
-            // Plain scale: matrix phases at wave priority 1 and the softmax at
-            // 0, so that a wavefront ready for MFMAs issues first when the two
-            // wavefronts of a SIMD drift apart (measured +1-2 %; with a
-            // score_mod the longer softmax is better left at equal priority).
             if (MOD == MOD_PLAIN) __builtin_amdgcn_s_setprio(1);
             w.qk(stage);
             if (MOD == MOD_PLAIN) __builtin_amdgcn_s_setprio(0);
@@ -906,19 +812,18 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
             w.pv(stage);
             if (MOD == MOD_PLAIN) __builtin_amdgcn_s_setprio(0);
         }
-        if (it + 1 < ntiles) w.store_tile(((it + 1) & 1) * L::STAGE);
-        if (it + 2 < ntiles) w.load_tile(w.tile_of(e_nn));
+        wait_vm_loads();
+        if (it + 1 < ntiles) w.zero_tail(w.tile_of(e_nxt), nstage);
+        __syncthreads();
         e_cur = e_nxt;
         e_nxt = e_nn;
-        e_nn = it + 3 < ntiles ? w.entry(it + 3) : 0;
-        __syncthreads();
     }
     w.store_output();
 }
 
 template <typename T, int D, int MOD, bool LIST, int NWAVES, bool PAIRED, int BN = kBlockN16, int SB = 1>
 __global__ __launch_bounds__(NWAVES * 64, 8 / NWAVES) void flash_fwd_lockstep_kernel(FwdArgs a) {
-    using L = TileLayout<D, BN * SB, !LIST>;
+    using L = TileLayout<D, BN * SB>;
     __shared__ __attribute__((aligned(16))) unsigned char smem[2 * L::STAGE];
     int bh, qts[2];
     const int n = work_tiles(a, PAIRED, bh, qts);
