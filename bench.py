@@ -38,7 +38,8 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="c3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cpu count)")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="0: the CPU affinity set, capped by OMP_NUM_THREADS when set")
     ap.add_argument("--cpu-heads", type=int, default=0, help="heads in the CPU sample; 0: two per thread")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="instead of attention, time a plain device-to-device copy of BYTES "
@@ -87,6 +88,16 @@ def traffic_from_profiles(w):
         return float(json.loads(p.read_text())["hbm_bytes_per_launch"])
     except (ValueError, KeyError):
         return None
+
+
+def host_threads() -> int:
+    """Host cores this process may use: its CPU affinity set, capped by
+    OMP_NUM_THREADS where the machine sets it (the CPU share of a GPU process)."""
+    n = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
 
 
 def cpu_baseline(w, threads: int, nheads: int, min_seconds: float = 10.0):
@@ -263,8 +274,11 @@ def main() -> int:
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        threads = args.cpu_threads or host_threads()
         rec["cpu_baseline"] = cpu_baseline(w, threads, args.cpu_heads)
+        rec["cpu_baseline"]["host_cpus"] = {"affinity": len(os.sched_getaffinity(0)),
+                                            "cpu_count": os.cpu_count(),
+                                            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
     print(json.dumps(rec))
     return 0
 

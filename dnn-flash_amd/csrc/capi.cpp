@@ -239,22 +239,27 @@ size_t workspace_bytes_for(const ofh_attention_params* p, const Resolved& r) {
     return n;
 }
 
-// Library-owned scratch per device, used when the caller passes no workspace.
+// Library-owned scratch, used when the caller passes no workspace: one buffer
+// per (device, stream). Calls on one stream run in stream order, so they can
+// share its buffer; calls on different streams never share one. The mutex is
+// held from the lookup until the call's launches are queued (fwd_impl), so a
+// buffer is grown (its stream synchronised, then freed) only when no launch
+// that uses it can still be unqueued.
 struct DeviceScratch {
     void* ptr = nullptr;
     size_t bytes = 0;
 };
 std::mutex g_scratch_mu;
-std::map<int, DeviceScratch> g_scratch;
+std::map<std::pair<int, hipStream_t>, DeviceScratch> g_scratch;
 
-int library_scratch(size_t bytes, void** out) {
+// Caller holds g_scratch_mu.
+int library_scratch_locked(size_t bytes, hipStream_t stream, void** out) {
     int dev = 0;
     OFH_HIP_CHECK(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    DeviceScratch& s = g_scratch[dev];
+    DeviceScratch& s = g_scratch[{dev, stream}];
     if (s.bytes < bytes) {
         if (s.ptr != nullptr) {
-            OFH_HIP_CHECK(hipDeviceSynchronize());  // earlier launches may still use it
+            OFH_HIP_CHECK(hipStreamSynchronize(stream));  // earlier launches on this stream may still use it
             OFH_HIP_CHECK(hipFree(s.ptr));
             s.ptr = nullptr;
             s.bytes = 0;
@@ -323,9 +328,12 @@ int fwd_impl(const ofh_attention_params* p, const void* q, const void* k, const 
     }
     const size_t need = workspace_bytes_for(p, r);
     void* ws = workspace;
+    // held until this call's launches are queued when it uses library scratch
+    std::unique_lock<std::mutex> scratch_lock(g_scratch_mu, std::defer_lock);
     if (need > 0) {
         if (ws == nullptr) {
-            if (int rc = library_scratch(need, &ws)) return rc;
+            scratch_lock.lock();
+            if (int rc = library_scratch_locked(need, stream, &ws)) return rc;
         } else if (workspace_bytes < need) {
             return set_error(OFH_ERROR_WORKSPACE_TOO_SMALL,
                              "workspace too small: need " + std::to_string(need) + " bytes");

@@ -236,26 +236,103 @@ def dtype_code(t) -> int:
     return {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16}[t]
 
 
+def _check_attention_inputs(q, k, v, mask, mask_block_size, alibi_slopes, bias, out, out_dtype,
+                            workspace):
+    """Raises ValueError for any argument the kernels would read or write out of
+    bounds: shapes, dtypes, devices and layouts are checked before a pointer
+    reaches the C ABI (the checks of the TensorFlow op, onednn_flash_attention_op.cc)."""
+    torch = _torch()
+    floats = (torch.float32, torch.bfloat16, torch.float16)
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not isinstance(t, torch.Tensor) or t.dim() != 4:
+            raise ValueError(f"{name} must be a rank-4 [B,H,T,D] tensor")
+        if t.dtype not in floats:
+            raise ValueError(f"{name} must be float32, bfloat16 or float16")
+        if t.stride(-1) != 1 or min(t.stride()) < 0:
+            raise ValueError(f"{name}: last axis must be contiguous and strides non-negative")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k and v must share one dtype")
+    B, H, M, D = q.shape
+    if tuple(k.shape[:2]) != (B, H) or tuple(v.shape[:2]) != (B, H):
+        raise ValueError("q, k and v must have the same batch and head dimensions")
+    if k.shape[3] != D:
+        raise ValueError("q/k head dimensions must match")
+    if v.shape[2] != k.shape[2]:
+        raise ValueError("k/v key-token dimensions must match")
+    N, Dv = k.shape[2], v.shape[3]
+    dev = q.device
+    tensors = [("k", k), ("v", v)]
+    if mask is not None:
+        if not isinstance(mask, torch.Tensor) or mask.dtype != torch.uint8 or mask.dim() != 2:
+            raise ValueError("mask must be a 2-D uint8 tensor [query_blocks, key_blocks]")
+        if not mask.is_contiguous():
+            raise ValueError("mask must be contiguous")
+        if len(mask_block_size) != 2 or min(int(x) for x in mask_block_size) <= 0:
+            raise ValueError("mask_block_size must be two positive integers")
+        tensors.append(("mask", mask))
+    if alibi_slopes is not None and bias is not None:
+        raise ValueError("pass either alibi_slopes or bias, not both")
+    if alibi_slopes is not None:
+        if alibi_slopes.dtype != torch.float32 or alibi_slopes.dim() != 1 or alibi_slopes.shape[0] != H:
+            raise ValueError("alibi_slopes must be a float32 tensor of length H")
+        if not alibi_slopes.is_contiguous():
+            raise ValueError("alibi_slopes must be contiguous")
+        tensors.append(("alibi_slopes", alibi_slopes))
+    if bias is not None:
+        if bias.dtype != torch.float32:
+            raise ValueError("bias must be float32")
+        if bias.dim() == 2:
+            if tuple(bias.shape) != (M, N) or not bias.is_contiguous():
+                raise ValueError("a shared bias must be a contiguous [M, N] tensor")
+        elif bias.dim() == 4:
+            if tuple(bias.shape) != (B, H, M, N) or bias.stride(-1) != 1 or min(bias.stride()) < 0:
+                raise ValueError("a per-head bias must be [B, H, M, N] with a contiguous last axis")
+        else:
+            raise ValueError("bias must be [M, N] or [B, H, M, N]")
+        tensors.append(("bias", bias))
+    if out is not None:
+        if tuple(out.shape) != (B, H, M, Dv):
+            raise ValueError(f"out must have shape {(B, H, M, Dv)}")
+        if out.dtype not in (q.dtype, torch.float32):
+            raise ValueError("out must have the dtype of q or float32")
+        if out_dtype is not None and out.dtype != out_dtype:
+            raise ValueError("out and out_dtype disagree")
+        if out.stride(-1) != 1 or min(out.stride()) < 0:
+            raise ValueError("out: last axis must be contiguous and strides non-negative")
+        tensors.append(("out", out))
+    elif out_dtype is not None and out_dtype not in (q.dtype, torch.float32):
+        raise ValueError("out_dtype must be the dtype of q or float32")
+    if workspace is not None:
+        if workspace.dtype != torch.uint8 or not workspace.is_contiguous():
+            raise ValueError("workspace must be a contiguous uint8 tensor")
+        tensors.append(("workspace", workspace))
+    if dev.type != "cuda":
+        raise ValueError("q must be a GPU tensor")
+    for name, t in tensors:
+        if t.device != dev:
+            raise ValueError(f"{name} must be on {dev}")
+
+
 def attention_fwd(q, k, v, *, scale: float | None = None, causal: bool = False, mask=None,
                   mask_block_size: tuple[int, int] = (1, 1), alibi_slopes=None, bias=None,
                   softcap: float = 0.0, out=None, out_dtype=None, algorithm: int = ALGO_AUTO,
                   workspace=None, stream=None):
     """q: [B,H,M,D], k: [B,H,N,D], v: [B,H,N,Dv] device tensors (f32/bf16/f16, last
     axis contiguous). mask: uint8 device tensor [qblocks, kblocks]. alibi_slopes:
-    f32 device [H]. bias: f32 device [M,N] (shared) or [B,H,M,N]. Returns out."""
+    f32 device [H]. bias: f32 device [M,N] (shared) or [B,H,M,N]. Returns out.
+    Raises ValueError before any launch when the arguments do not fit together."""
     torch = _torch()
+    _check_attention_inputs(q, k, v, mask, mask_block_size, alibi_slopes, bias, out, out_dtype,
+                            workspace)
     B, H, M, D = q.shape
     N, Dv = k.shape[2], v.shape[3]
-    for t in (q, k, v):
-        if t.stride(-1) != 1:
-            raise ValueError("last axis must be contiguous")
     if out is None:
         out = torch.empty((B, H, M, Dv), device=q.device,
                           dtype=q.dtype if out_dtype is None else out_dtype)
     kw = {}
     if mask is not None:
-        kw.update(mask_allowed=mask.data_ptr(), mask_query_block_size=mask_block_size[0],
-                  mask_key_block_size=mask_block_size[1], mask_query_blocks=mask.shape[0],
+        kw.update(mask_allowed=mask.data_ptr(), mask_query_block_size=int(mask_block_size[0]),
+                  mask_key_block_size=int(mask_block_size[1]), mask_query_blocks=mask.shape[0],
                   mask_key_blocks=mask.shape[1])
     bias_kind = BIAS_NONE
     if alibi_slopes is not None:

@@ -168,9 +168,23 @@ public:
         ofh_attention_params p;
         if (!prepare(ctx, dtype_code<T>(), &out, &p)) return;
         void* stream = (void*)ctx->eigen_device<Eigen::GpuDevice>().stream();
+        // Scratch (block-mask tile lists, key-split partial rows) comes from
+        // TensorFlow's allocator, so the library neither allocates nor blocks
+        // the host inside Compute.
+        size_t ws_bytes = 0;
+        if (ofh_attention_workspace_bytes(&p, &ws_bytes) != OFH_SUCCESS) {
+            fail(ctx);
+            return;
+        }
+        Tensor ws;
+        void* ws_ptr = nullptr;
+        if (ws_bytes > 0) {
+            OP_REQUIRES_OK(ctx, ctx->allocate_temp(DT_UINT8, TensorShape({(int64_t)ws_bytes}), &ws));
+            ws_ptr = ws.flat<uint8_t>().data();
+        }
         const int rc = ofh_attention_fwd(&p, ctx->input(0).flat<T>().data(), ctx->input(1).flat<T>().data(),
-                                         ctx->input(2).flat<T>().data(), out->flat<T>().data(), nullptr, 0,
-                                         stream);
+                                         ctx->input(2).flat<T>().data(), out->flat<T>().data(), ws_ptr,
+                                         ws_bytes, stream);
         if (rc != OFH_SUCCESS) fail(ctx);
     }
 };

@@ -119,13 +119,15 @@ void ofh_attention_params_init(ofh_attention_params* p);
 int ofh_attention_workspace_bytes(const ofh_attention_params* p, size_t* bytes);
 
 /* Attention forward on device buffers, ordered on `stream` (asynchronous).
- * workspace may be NULL: the library then uses a per-device buffer it owns,
- * grown on demand (one hipMalloc the first time a larger size is needed, after
- * a device synchronisation if an older buffer is replaced). Calls captured
- * into a HIP graph should pass a workspace of ofh_attention_workspace_bytes
- * bytes, or follow an uncaptured call of the same shape, so that no growth
- * happens during capture. Calls sharing the library's buffer must be ordered
- * (one stream, or synchronised streams).
+ * workspace may be NULL: the library then uses a buffer it owns, one per
+ * (device, stream), grown on demand: the first call that needs more than the
+ * buffer holds synchronises that stream (hipStreamSynchronize), frees the old
+ * buffer and calls hipMalloc. Such a call blocks the host, so callers that
+ * must not block or allocate (HIP graph capture, framework ops with their own
+ * allocator) pass a workspace of ofh_attention_workspace_bytes bytes instead.
+ * Calls from several host threads are safe: a thread holds the library's lock
+ * from choosing the buffer until its launches are queued, and calls on
+ * different streams never share a buffer.
  * Fully-masked query rows are written as zeros, as standard_attention leaves
  * them (attention.cpp:111-113). */
 int ofh_attention_fwd(const ofh_attention_params* p, const void* q, const void* k,

@@ -15,7 +15,13 @@ import numpy as np
 from oracle import oracle as O
 
 TOL = {"f32": 1e-4, "bf16": 2e-2, "f16": 2e-2}
-THREADS = min(16, os.cpu_count() or 1)
+def _host_threads() -> int:
+    n = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(n, int(omp)) if omp.isdigit() and int(omp) > 0 else n)
+
+
+THREADS = _host_threads()
 
 
 def torch_dtype(dt: str):

@@ -239,3 +239,49 @@ def test_workspace_bytes(ofh):
                       mask_key_blocks=8)
     nqt, nkt = 4, 8  # 128-row query tiles (block-mask schedule), 64-key tiles
     assert F.workspace_bytes(p) == 256 + nqt * nkt * 4
+
+
+def test_attention_fwd_rejects_mismatched_inputs_before_launch(ofh):
+    """attention_fwd checks shapes, dtypes, devices and layouts and raises
+    ValueError before any pointer reaches the C ABI (CPU tensors: no launch can
+    happen; every case below fails on its own mismatch first)."""
+    torch = pytest.importorskip("torch")
+    B, H, M, N, D = 2, 3, 8, 10, 16
+
+    def t(*shape, dtype=torch.bfloat16):
+        return torch.zeros(shape, dtype=dtype)
+
+    q, k, v = t(B, H, M, D), t(B, H, N, D), t(B, H, N, D)
+    cases = [
+        (dict(q=t(B, H, M)), "rank-4"),
+        (dict(q=t(B, H, M, D, dtype=torch.float64)), "float32, bfloat16 or float16"),
+        (dict(k=t(B, H, N, D, dtype=torch.float16)), "share one dtype"),
+        (dict(k=t(B, H + 1, N, D)), "same batch and head"),
+        (dict(v=t(B + 1, H, N, D)), "same batch and head"),
+        (dict(k=t(B, H, N, D + 8)), "head dimensions must match"),
+        (dict(v=t(B, H, N + 1, D)), "key-token dimensions must match"),
+        (dict(q=t(B, H, D, M).transpose(2, 3)), "last axis must be contiguous"),
+        (dict(mask=t(2, 2, dtype=torch.int32)), "uint8"),
+        (dict(mask=t(4, 2, dtype=torch.uint8).t()), "contiguous"),
+        (dict(mask=t(2, 2, dtype=torch.uint8), mask_block_size=(0, 4)), "positive"),
+        (dict(alibi_slopes=t(H + 1, dtype=torch.float32)), "length H"),
+        (dict(alibi_slopes=t(H, dtype=torch.float16)), "length H"),
+        (dict(alibi_slopes=t(H, dtype=torch.float32), bias=t(M, N, dtype=torch.float32)), "not both"),
+        (dict(bias=t(M, N)), "float32"),
+        (dict(bias=t(M, N + 1, dtype=torch.float32)), "[M, N]"),
+        (dict(bias=t(N, M, dtype=torch.float32).t()), "[M, N]"),
+        (dict(bias=t(B, H, M, N + 1, dtype=torch.float32)), "[B, H, M, N]"),
+        (dict(bias=t(H, M, N, dtype=torch.float32)), "[M, N] or [B, H, M, N]"),
+        (dict(out=t(B, H, M + 1, D)), "out must have shape"),
+        (dict(out=t(B, H, M, D, dtype=torch.float16)), "dtype of q or float32"),
+        (dict(out=t(B, H, M, D), out_dtype=torch.float32), "disagree"),
+        (dict(out_dtype=torch.float16), "dtype of q or float32"),
+        (dict(workspace=t(16, dtype=torch.float32)), "uint8"),
+        ({}, "GPU tensor"),
+    ]
+    for over, msg in cases:
+        args = dict(q=q, k=k, v=v)
+        args.update(over)
+        qq, kk, vv = args.pop("q"), args.pop("k"), args.pop("v")
+        with pytest.raises(ValueError, match=re.escape(msg)):
+            ofh.attention_fwd(qq, kk, vv, **args)

@@ -296,6 +296,55 @@ def test_host_entry_point(ofh):
         check(out, ref, dt, f"host entry {dt}")
 
 
+def test_library_scratch_concurrent_threads_growing(ofh):
+    """Device entry with workspace=NULL from several host threads at once, each
+    on its own stream, with the scratch need growing call by call (block-mask
+    tile lists over longer key ranges, fp32 key-split partial rows): the
+    library's buffer for a stream is replaced only after that stream's queued
+    work is done, and streams never share one. Every result meets the bar."""
+    import threading
+    F = ofh
+    rng = np.random.default_rng(5)
+    shapes = [(128, 512), (128, 1536), (256, 4096), (96, 8192)]
+    jobs = []
+    for t in range(4):
+        per = []
+        for i, (M, N) in enumerate(shapes):
+            dt = "f32" if (t + i) % 2 else "bf16"
+            dev, host = make_inputs(dt, 1, 2, M, N, 64, seed=40 + 4 * t + i)
+            mask = (rng.random((-(-M // 64), -(-N // 64))) < 0.5).astype(np.uint8)
+            mask[:, 0] = 1
+            ref = oracle_full(host, mask=mask, mbs=(64, 64)) if dt == "bf16" else oracle_full(host)
+            per.append((dt, dev, mask, ref))
+        jobs.append(per)
+    errors, results = [], {}
+
+    def work(t):
+        try:
+            stream = torch.cuda.Stream()
+            with torch.cuda.stream(stream):
+                for i, (dt, dev, mask, ref) in enumerate(jobs[t]):
+                    kw = {}
+                    if dt == "bf16":
+                        kw = dict(mask=torch.from_numpy(mask).cuda(), mask_block_size=(64, 64))
+                    for _ in range(3):
+                        out = F.attention_fwd(*dev, out_dtype=torch.float32, **kw)
+                    stream.synchronize()
+                    results[(t, i)] = out.cpu().numpy()
+        except Exception as e:  # reported below, on the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=work, args=(t,)) for t in range(len(jobs))]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors, errors
+    for t, per in enumerate(jobs):
+        for i, (dt, _, _, ref) in enumerate(per):
+            check(results[(t, i)], ref, dt, f"thread {t} call {i} {dt}")
+
+
 def test_host_entry_concurrent_threads(ofh):
     """Host threads calling the host entry at the same time each get their own
     staging and attention workspace (key-split partial rows, tile lists): every
@@ -406,3 +455,84 @@ def test_workload_full_size(ofh, name):
         _sampled_check(ofh, w, rows_per_head=w.tokens, heads=w.batch * w.heads)
     else:
         _sampled_check(ofh, w)
+
+
+# ---------------------------------------------------------------------------
+# Online-softmax rescaling with a live accumulator. With N(0,1) inputs and
+# scale 1/sqrt(D) no key tile beats the running max by the lazy-rescale slack
+# after the first tile, so the rescale of a non-zero O and l (the recurrence
+# of attention.cpp:628-673) would go unexercised. These inputs put the scores
+# in key regions: A (keys [0, N/4)) at 0, S1 ([N/4, N/2)) at +d1, S2 (2 keys
+# at N/2) at +d2 = d1 + 9.5, C (the rest) at 0, in log2 units, with the noise
+# of the other dimensions kept small (std 0.3). d1 = 8.5 forces a raise of the
+# running max while O holds A, d2 another while O holds A + S1; S1 and S2 carry
+# comparable probability mass and V rows offset by region (+1, -1, +2, 0), so a
+# wrong or missing rescale of O or l moves the output far beyond tolerance.
+
+
+def rescale_inputs(dt, B, H, M, N, D, seed, sign=1.0, d1=8.5):
+    scale = sign / math.sqrt(D)
+    rng_std = 0.3
+    q = O.normal(3 * seed + 1, (B, H, M, D), std=rng_std)
+    k = O.normal(3 * seed + 2, (B, H, N, D), std=rng_std)
+    v = O.normal(3 * seed + 3, (B, H, N, D))
+    a = 4.0
+    unit = a * abs(scale) * 1.4426950408889634  # log2 units per unit of k[..., 0]
+    s1, s2 = N // 4, N // 2
+    lvl = np.zeros(N, np.float32)
+    lvl[s1:s2] = d1
+    lvl[s2:s2 + 2] = d1 + 9.5
+    q[..., 0] = a
+    k[..., 0] = sign * lvl / unit  # scale * q0 * k0 = lvl / log2(e)
+    off = np.zeros(N, np.float32)
+    off[:s1], off[s1:s2], off[s2:s2 + 2] = 1.0, -1.0, 2.0
+    v += off[None, None, :, None]
+    tq, uq = to_device(q, dt)
+    tk, uk = to_device(k, dt)
+    tv, uv = to_device(v, dt)
+    return (tq, tk, tv), (uq, uk, uv), scale
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_rescale_with_live_accumulator(ofh, dt, D, sign):
+    """Plain-scale kernels (bf16/fp16: the D=64 128-key tile, the D=128 tile
+    staged as two 64-key steps; fp32), causal (paired query tiles) and not,
+    and a negative scale (the min-based raw max of the unmasked tiles)."""
+    N = 2048
+    for causal, M in ((False, 300), (True, N)):
+        dev, host, scale = rescale_inputs(dt, 1, 2, M, N, D, seed=D + int(sign > 0), sign=sign)
+        out = run(ofh, dev, dt=dt, causal=causal, scale=scale)
+        ref = oracle_full(host, causal=causal, scale=scale)
+        check(out, ref, dt, f"{dt} D{D} rescale causal={causal} scale={scale:+.4f}")
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_rescale_with_live_accumulator_block_mask(ofh, dt, sign):
+    """The same for the block-mask list kernels (64-key tiles, per-wavefront
+    skip bits): a dense 64x64 bitmap with a few blocks of region C removed."""
+    N, D = 2048, 64
+    qb = kb = N // 64
+    mask = np.ones((qb, kb), np.uint8)
+    mask[:, kb - 3] = 0
+    mask[5, 20] = 0
+    for causal, M in ((False, 300), (True, N)):
+        dev, host, scale = rescale_inputs(dt, 1, 2, M, N, D, seed=7, sign=sign)
+        mq = -(-M // 64)
+        out = run(ofh, dev, dt=dt, causal=causal, scale=scale, mask=mask[:mq], mbs=(64, 64))
+        ref = oracle_full(host, causal=causal, scale=scale, mask=mask[:mq], mbs=(64, 64))
+        check(out, ref, dt, f"{dt} list rescale causal={causal} scale={scale:+.4f}")
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_rescale_with_score_mod(ofh, dt):
+    """The score_mod kernel (ALiBi + soft-cap) on the same inputs."""
+    N, D, H = 2048, 128, 2
+    slopes = np.array([1e-3, 2e-3], np.float32)
+    for causal, M in ((False, 300), (True, N)):
+        dev, host, scale = rescale_inputs(dt, 1, H, M, N, D, seed=9)
+        out = run(ofh, dev, dt=dt, causal=causal, scale=scale, slopes=slopes, softcap=50.0)
+        ref = oracle_full(host, causal=causal, scale=scale, slopes=slopes, softcap=50.0)
+        check(out, ref, dt, f"{dt} score_mod rescale causal={causal}")
