@@ -131,6 +131,14 @@ def lib() -> ctypes.CDLL:
     """Loads the shared library (raises if it was not built)."""
     global _lib
     if _lib is None:
+        # torch links its own copy of the HIP runtime under another file name;
+        # loaded after this library it would start a second runtime in the
+        # process, and this library's would then see no device. Importing
+        # torch first makes the library bind the runtime torch already loaded.
+        try:
+            import torch  # noqa: F401, PLC0415
+        except ImportError:
+            pass
         if not LIB_PATH.exists():
             raise FileNotFoundError(
                 f"{LIB_PATH} is missing: build it with `make -C dnn-flash_amd` "

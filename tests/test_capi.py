@@ -7,6 +7,7 @@ from __future__ import annotations
 import ctypes
 import re
 import subprocess
+import sys
 from pathlib import Path
 
 import numpy as np
@@ -285,3 +286,21 @@ def test_attention_fwd_rejects_mismatched_inputs_before_launch(ofh):
         qq, kk, vv = args.pop("q"), args.pop("k"), args.pop("v")
         with pytest.raises(ValueError, match=re.escape(msg)):
             ofh.attention_fwd(qq, kk, vv, **args)
+
+
+def test_one_hip_runtime_when_the_library_loads_before_torch():
+    """Loading the library first must not leave two HIP runtimes in the process
+    (torch's bundled copy and /opt/rocm's): the binding imports torch before
+    it loads the library, so both use the one torch loaded."""
+    pytest.importorskip("torch")
+    code = (
+        "import sys; sys.path.insert(0, %r)\n"
+        "import onednn_flash_hip as F\n"
+        "F.lib()\n"
+        "import torch\n"
+        "maps = {l.split()[-1] for l in open('/proc/self/maps') if 'libamdhip64' in l}\n"
+        "print(len(maps), sorted(maps))\n"
+    ) % str(ROOT / "dnn-flash_amd" / "python")
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.startswith("1 "), out.stdout
