@@ -434,6 +434,24 @@ int ofh_attention_fwd(const ofh_attention_params* p, const void* q, const void* 
     return fwd_impl(p, q, k, v, out, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
+int ofh_attention_fwd_noalloc(const ofh_attention_params* p, const void* q, const void* k,
+                              const void* v, void* out, void* stream) {
+    if (int rc = validate(p, true, q, k, v, out)) return rc;
+    Resolved r;
+    if (int rc = resolve(p, q, k, v, out, r)) return rc;
+    const size_t need = r.algorithm == OFH_ALGO_FLASH_MFMA ? workspace_bytes_for(p, r) : 0;
+    if (need > ofh::kNoAllocScratchBytes)
+        return set_error(OFH_ERROR_WORKSPACE_TOO_SMALL,
+                         "ofh_attention_fwd_noalloc: this call needs " + std::to_string(need) +
+                             " bytes of scratch; the allocation-free entry holds at most " +
+                             std::to_string(ofh::kNoAllocScratchBytes) +
+                             " (use ofh_attention_fwd with a workspace)");
+    void* ws = nullptr;
+    if (need > 0) OFH_HIP_CHECK(ofh::noalloc_scratch(&ws));
+    return fwd_impl(p, q, k, v, out, ws, need > 0 ? ofh::kNoAllocScratchBytes : 0,
+                    static_cast<hipStream_t>(stream));
+}
+
 int ofh_attention_fwd_host(const ofh_attention_params* p, const float* q, const float* k,
                            const float* v, float* out) {
     if (int rc = validate(p, true, q, k, v, out)) return rc;

@@ -118,4 +118,10 @@ const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile
 // Workgroup tiling of the MFMA kernel for a dtype.
 MfmaTiles flash_mfma_tiles(int dtype, int head_dim, bool general_mod, bool tile_list, bool causal);
 
+// Scratch of the allocation-free entry point: a static device array of
+// kNoAllocScratchBytes per GPU. noalloc_scratch returns the current device's
+// address of it (looked up once per device, then cached).
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+hipError_t noalloc_scratch(void** ptr);
+
 }  // namespace ofh

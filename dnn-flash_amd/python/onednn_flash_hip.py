@@ -36,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "ofh_attention_params_init",
     "ofh_attention_workspace_bytes",
     "ofh_attention_fwd",
+    "ofh_attention_fwd_noalloc",
     "ofh_attention_fwd_host",
     "ofh_attention_launch_info",
     "ofh_attention_useful_flops",
@@ -149,6 +150,7 @@ def lib() -> ctypes.CDLL:
         L.ofh_attention_params_init.restype = None
         L.ofh_attention_workspace_bytes.argtypes = [P, ctypes.POINTER(ctypes.c_size_t)]
         L.ofh_attention_fwd.argtypes = [P] + [ctypes.c_void_p] * 5 + [ctypes.c_size_t, ctypes.c_void_p]
+        L.ofh_attention_fwd_noalloc.argtypes = [P] + [ctypes.c_void_p] * 5
         L.ofh_attention_fwd_host.argtypes = [P] + [ctypes.c_void_p] * 4
         L.ofh_attention_launch_info.argtypes = [P, ctypes.POINTER(LaunchInfo)]
         L.ofh_attention_useful_flops.argtypes = [P, ctypes.POINTER(ctypes.c_double)]
@@ -160,7 +162,8 @@ def lib() -> ctypes.CDLL:
         L.ofh_last_error.restype = ctypes.c_char_p
         L.ofh_last_error.argtypes = []
         L.ofh_abi_version.restype = ctypes.c_int
-        for fn in ("ofh_attention_workspace_bytes", "ofh_attention_fwd", "ofh_attention_fwd_host",
+        for fn in ("ofh_attention_workspace_bytes", "ofh_attention_fwd", "ofh_attention_fwd_noalloc",
+                   "ofh_attention_fwd_host",
                    "ofh_attention_launch_info", "ofh_attention_useful_flops"):
             getattr(L, fn).restype = ctypes.c_int
         _lib = L

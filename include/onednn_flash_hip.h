@@ -134,6 +134,21 @@ int ofh_attention_fwd(const ofh_attention_params* p, const void* q, const void* 
                       const void* v, void* out, void* workspace, size_t workspace_bytes,
                       void* stream);
 
+/* ofh_attention_fwd without a workspace argument and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory inside the call (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Its scratch (block-mask tile lists,
+ * key-split partial rows) is a static device array of 16 MiB (16777216 bytes)
+ * that every GPU the library runs on holds until the process ends; calls that
+ * need more scratch than that (ofh_attention_workspace_bytes) fail with
+ * OFH_ERROR_WORKSPACE_TOO_SMALL before any launch. It calls no hipMalloc or
+ * hipFree; the first call on a device looks up that device's address of the
+ * array once. All calls on one GPU share the array: calls that overlap on one
+ * GPU (other streams, other host threads without ordering) race on it and
+ * must be serialised by the caller. */
+int ofh_attention_fwd_noalloc(const ofh_attention_params* p, const void* q, const void* k,
+                              const void* v, void* out, void* stream);
+
 /* The same computation on host fp32 buffers (contiguous reference layout):
  * copies in, runs on the current device, copies out, synchronises. The dtype
  * field selects the precision the GPU computes in (inputs are rounded to it

@@ -1,0 +1,95 @@
+"""The allocation-free entry point ofh_attention_fwd_noalloc (no counterpart in
+the reference; for callers that cannot allocate inside the call): through the
+C ABI, against ofh_attention_fwd on the same inputs, for the calls that use
+scratch (block-mask tile lists, fp32 key-split partial rows), twice in a row
+with the second call smaller, plus its size limit."""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+
+from gpu_helpers import TOL, make_inputs, norm_error
+from oracle import oracle as O
+
+NOALLOC_MAX = 16 << 20
+
+
+def test_noalloc_rejects_oversized_scratch(ofh):
+    """A call whose scratch exceeds the static array fails before any launch
+    (fake 16-byte-aligned pointers: nothing is dereferenced or launched)."""
+    F = ofh
+    M, N = 131072, 524288
+    p = F.make_params(1, 1, M, N, 64, dtype=F.DTYPE_BF16, mask_allowed=4096,
+                      mask_query_block_size=64, mask_key_block_size=64,
+                      mask_query_blocks=M // 64, mask_key_blocks=N // 64)
+    assert F.workspace_bytes(p) > NOALLOC_MAX
+    rc = F.lib().ofh_attention_fwd_noalloc(ctypes.byref(p), 16, 32, 48, 64, None)
+    assert rc == F.OFH_ERROR_WORKSPACE_TOO_SMALL
+    msg = F.lib().ofh_last_error().decode()
+    assert "at most 16777216" in msg and str(F.workspace_bytes(p)) in msg
+
+
+def _window_mask(M, N, bs=64, window=4, sinks=1):
+    qb, kb = -(-M // bs), -(-N // bs)
+    i, j = np.meshgrid(np.arange(qb), np.arange(kb), indexing="ij")
+    return ((j <= i) & ((i - j < window) | (j < sinks))).astype(np.uint8)
+
+
+@pytest.mark.gpu
+def test_noalloc_matches_fwd(ofh):
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    F = ofh
+    lib = F.lib()
+    cases = [  # (label, dtype, B, H, M, N, D, causal, block mask?)
+        ("bf16 block mask", "bf16", 1, 4, 4096, 4096, 64, True, True),
+        ("bf16 block mask, smaller", "bf16", 1, 2, 1024, 1024, 64, True, True),
+        ("fp32 key split", "f32", 1, 4, 512, 1024, 64, False, False),
+        ("fp32 key split, smaller", "f32", 1, 2, 128, 640, 128, True, False),
+    ]
+    stream = torch.cuda.Stream()
+    free_after_first = None
+    for i, (label, dt, B, H, M, N, D, causal, masked) in enumerate(cases):
+        dev, host = make_inputs(dt, B, H, M, N, D, seed=60 + i)
+        q, k, v = dev
+        kw = {}
+        mask = mask_t = None
+        if masked:
+            mask = _window_mask(M, N)
+            mask_t = torch.from_numpy(mask).cuda()
+            kw = dict(mask_allowed=mask_t.data_ptr(), mask_query_block_size=64,
+                      mask_key_block_size=64, mask_query_blocks=mask.shape[0],
+                      mask_key_blocks=mask.shape[1])
+        code = {"f32": F.DTYPE_F32, "bf16": F.DTYPE_BF16}[dt]
+        p = F.make_params(B, H, M, N, D, dtype=code, out_dtype=F.DTYPE_F32, scale=1.0 / math.sqrt(D),
+                          causal=causal, **kw)
+        need = F.workspace_bytes(p)
+        assert 0 < need <= NOALLOC_MAX, (label, need)
+        o_ref = torch.empty((B, H, M, D), device="cuda", dtype=torch.float32)
+        o_na = torch.full_like(o_ref, float("nan"))
+        torch.cuda.synchronize()
+        print(f"case {label}: B{B} H{H} M{M} N{N} D{D} scratch {need} bytes", flush=True)
+        F.check(lib.ofh_attention_fwd(ctypes.byref(p), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                      o_ref.data_ptr(), None, 0, stream.cuda_stream))
+        stream.synchronize()
+        free0 = torch.cuda.mem_get_info()[0]
+        for _ in range(2):
+            F.check(lib.ofh_attention_fwd_noalloc(ctypes.byref(p), q.data_ptr(), k.data_ptr(),
+                                                  v.data_ptr(), o_na.data_ptr(), stream.cuda_stream))
+        stream.synchronize()
+        free1 = torch.cuda.mem_get_info()[0]
+        if free_after_first is not None:
+            assert free1 == free0, f"{label}: device memory changed by {free0 - free1} bytes"
+        free_after_first = free1
+        a, b = o_ref.cpu().numpy(), o_na.cpu().numpy()
+        assert np.array_equal(a, b), f"{label}: differs from ofh_attention_fwd (max {np.nanmax(np.abs(a - b))})"
+        prob = O.Problem(B, H, M, N, D, D, scale=1.0 / math.sqrt(D), causal=causal, mask=mask,
+                         mask_query_block_size=64, mask_key_block_size=64)
+        err, maxabs = norm_error(b, O.standard_attention(*host, prob))
+        print(f"{label}: identical to ofh_attention_fwd; vs oracle normwise {err:.3e} max-abs {maxabs:.3e}")
+        assert err <= TOL[dt]
