@@ -119,42 +119,62 @@ int validate(const ofh_attention_params* p, bool check_ptrs, const void* q, cons
         return set_error(OFH_ERROR_INVALID_ARGUMENT, "softcap must be finite and >= 0");
     if (p->algorithm < OFH_ALGO_AUTO || p->algorithm > OFH_ALGO_ROWWISE)
         return set_error(OFH_ERROR_INVALID_ARGUMENT, "unknown algorithm");
+    if (p->max_key_splits < 0)
+        return set_error(OFH_ERROR_INVALID_ARGUMENT, "max_key_splits must be >= 0");
     return OFH_SUCCESS;
 }
 
-// Key split of the fp32 kernel (one wavefront per SIMD, 128 query rows per
-// workgroup). A call with fewer query-tile workgroups than two per CU leaves
-// the chip idle, and causal calls are bound by their longest query tile; such
-// calls run the K/V tile steps of each query tile in ranges of split_tiles
-// (at least 64 keys) sized so that all ranges together fill about 512 workgroups,
-// then merge the partial rows. Without a mask the tile steps of query tile qt
-// are known on the host; with a block mask the list can only remove steps, so
-// the unmasked count is an upper bound.
+// Key split. A call whose query tiles give fewer workgroups than kTarget
+// leaves CUs idle and runs as long as its longest query tile: the decode and
+// short-query shapes (M <= 256 rows per head) of the 16-bit kernels, small
+// fp32 calls. Such calls run the K/V tile steps of each query tile in ranges
+// of split_tiles steps (at least 64 keys) sized so that all ranges together
+// fill about kTarget workgroups, then merge the partial rows. Causal 16-bit
+// calls then run their query tiles unpaired. Without a mask the tile steps of
+// query tile qt are known on the host; with a block mask the list can only
+// remove steps, so the unmasked count is an upper bound.
 void choose_key_splits(const ofh_attention_params* p, Resolved& r) {
     r.key_splits = 1;
     r.split_tiles = 1 << 30;
-    if (p->dtype != OFH_DTYPE_F32 || r.paired) return;
-    constexpr int64_t kTargetWorkgroups = 512;
-    constexpr int kMaxSplits = 64;
+    if (p->dtype == OFH_DTYPE_F32 && r.paired) return;
+    if (p->max_key_splits == 1) return;
+    constexpr int64_t kTarget = 512;
+    const int kMaxSplits = p->max_key_splits > 1 ? std::min(p->max_key_splits, 64) : 64;
     const int64_t bh = (int64_t)p->batch * p->heads;
-    if (bh * r.num_q_tiles >= kTargetWorkgroups) return;
-    int64_t total = 0;
-    int max_steps = 0;
-    for (int qt = 0; qt < r.num_q_tiles; ++qt) {
-        const int64_t kend = p->causal ? std::min<int64_t>((int64_t)p->key_tokens, (int64_t)(qt + 1) * r.block_m)
-                                       : (int64_t)p->key_tokens;
-        const int steps = (int)((kend + r.block_n - 1) / r.block_n);
-        total += steps;
-        max_steps = std::max(max_steps, steps);
-    }
-    total *= bh;
-    const int min_steps = std::max(1, 64 / r.block_n);  // at least 64 keys per split
-    const int per = (int)std::max<int64_t>(min_steps, (total + kTargetWorkgroups - 1) / kTargetWorkgroups);
-    int splits = (max_steps + per - 1) / per;
+    const int64_t wgs = bh * (r.paired ? (r.num_q_tiles + 1) / 2 : r.num_q_tiles);
+    if (wgs >= kTarget) return;
+    // splits and steps per split for K/V tiles of block_n keys, each split
+    // at least min_steps tile steps
+    auto plan = [&](int block_n, int min_steps, int& splits, int& per, int& max_steps) {
+        int64_t total = 0;
+        max_steps = 0;
+        for (int qt = 0; qt < r.num_q_tiles; ++qt) {
+            const int64_t kend = p->causal ? std::min<int64_t>((int64_t)p->key_tokens, (int64_t)(qt + 1) * r.block_m)
+                                           : (int64_t)p->key_tokens;
+            const int steps = (int)((kend + block_n - 1) / block_n);
+            total += steps;
+            max_steps = std::max(max_steps, steps);
+        }
+        total *= bh;
+        per = (int)std::max<int64_t>(min_steps, (total + kTarget - 1) / kTarget);
+        splits = std::min((max_steps + per - 1) / per, kMaxSplits);
+    };
+    int splits, per, max_steps;
+    plan(r.block_n, std::max(1, 64 / r.block_n), splits, per, max_steps);  // at least 64 keys per split
     if (splits <= 1) return;
-    splits = std::min(splits, kMaxSplits);
     r.key_splits = splits;
     r.split_tiles = (max_steps + splits - 1) / splits;
+    r.paired = false;
+}
+
+void no_key_split(const ofh_attention_params* p, Resolved& r) {
+    const ofh::MfmaTiles t =
+        ofh::flash_mfma_tiles(p->dtype, (int)p->head_dim, r.general_mod, r.tile_list, p->causal != 0);
+    r.key_splits = 1;
+    r.split_tiles = 1 << 30;
+    r.paired = t.paired;
+    r.block_n = t.block_n;
+    r.num_k_tiles = (int)((p->key_tokens + r.block_n - 1) / r.block_n);
 }
 
 int resolve(const ofh_attention_params* p, const void* q, const void* k, const void* v,
@@ -233,6 +253,46 @@ size_t list_bytes(const Resolved& r) {
 size_t partial_rows(const ofh_attention_params* p, const Resolved& r) {
     return (size_t)r.key_splits * p->batch * p->heads * p->query_tokens;
 }
+// Arrival counters of the single-launch split merge: slot 0 serves the
+// allocation-free entry point, slots 1.. one stream each (first come, first
+// served). A call that finds no free slot, or runs with OFH_SPLIT_MERGE=launch
+// in the environment, merges in a second launch instead.
+std::mutex g_counter_mu;
+std::map<std::pair<int, hipStream_t>, int> g_counter_slots;
+int g_next_counter_slot = 1;
+
+int split_counters_for(hipStream_t stream, bool noalloc, unsigned** out) {
+    *out = nullptr;
+    const char* env = std::getenv("OFH_SPLIT_MERGE");
+    if (env != nullptr && std::strcmp(env, "launch") == 0) return OFH_SUCCESS;
+    int slot = 0;
+    if (!noalloc) {
+        int dev = 0;
+        OFH_HIP_CHECK(hipGetDevice(&dev));
+        std::lock_guard<std::mutex> lock(g_counter_mu);
+        auto it = g_counter_slots.find({dev, stream});
+        if (it == g_counter_slots.end()) {
+            if (g_next_counter_slot >= ofh::kSplitCounterSlots) return OFH_SUCCESS;
+            it = g_counter_slots.emplace(std::make_pair(dev, stream), g_next_counter_slot++).first;
+        }
+        slot = it->second;
+    }
+    OFH_HIP_CHECK(ofh::split_counter_slot(slot, out));
+    return OFH_SUCCESS;
+}
+
+// The workgroup that arrives last merges its query tile alone, so the merge
+// is one CU's latency chain: measured, it beats a second launch only while
+// the tile's partial rows are few (at most 64 KiB; single-row decode,
+// B1 H8 N32768 D128: 35.8 us against 39.4 us) and loses on larger ones
+// (fp32 B1 H4 N512 D64, 8 splits of 128 rows: 32.3 us against 18.1 us).
+bool merge_in_launch(const ofh_attention_params* p, const Resolved& r) {
+    if (r.key_splits <= 1) return false;
+    const int64_t tile_floats = std::min<int64_t>(r.block_m, (int64_t)p->query_tokens) *
+                                (int64_t)p->value_dim * r.key_splits;
+    return (int64_t)p->batch * p->heads * r.num_q_tiles <= ofh::kMaxSplitTiles && tile_floats <= (1 << 14);
+}
+
 size_t workspace_bytes_for(const ofh_attention_params* p, const Resolved& r) {
     size_t n = list_bytes(r);
     if (r.key_splits > 1) n = round256(n) + round256(partial_rows(p, r) * p->value_dim * 4) + partial_rows(p, r) * 8;
@@ -251,6 +311,19 @@ struct DeviceScratch {
 };
 std::mutex g_scratch_mu;
 std::map<std::pair<int, hipStream_t>, DeviceScratch> g_scratch;
+
+// Caller holds g_scratch_mu. Bytes of the library scratch of (current device, stream).
+size_t library_scratch_bytes_locked(hipStream_t stream) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    auto it = g_scratch.find({dev, stream});
+    return it == g_scratch.end() ? 0 : it->second.bytes;
+}
+
+bool stream_capturing(hipStream_t stream) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(stream, &st) == hipSuccess && st == hipStreamCaptureStatusActive;
+}
 
 // Caller holds g_scratch_mu.
 int library_scratch_locked(size_t bytes, hipStream_t stream, void** out) {
@@ -317,7 +390,8 @@ ofh::FwdArgs make_args(const ofh_attention_params* p, const Resolved& r, const v
 }
 
 int fwd_impl(const ofh_attention_params* p, const void* q, const void* k, const void* v,
-             void* out, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+             void* out, void* workspace, size_t workspace_bytes, hipStream_t stream,
+             bool noalloc = false) {
     if (int rc = validate(p, true, q, k, v, out)) return rc;
     Resolved r;
     if (int rc = resolve(p, q, k, v, out, r)) return rc;
@@ -326,14 +400,22 @@ int fwd_impl(const ofh_attention_params* p, const void* q, const void* k, const 
         OFH_HIP_CHECK(ofh::launch_rowwise(a, p->dtype, stream));
         return OFH_SUCCESS;
     }
-    const size_t need = workspace_bytes_for(p, r);
+    size_t need = workspace_bytes_for(p, r);
     void* ws = workspace;
     // held until this call's launches are queued when it uses library scratch
     std::unique_lock<std::mutex> scratch_lock(g_scratch_mu, std::defer_lock);
     if (need > 0) {
         if (ws == nullptr) {
             scratch_lock.lock();
-            if (int rc = library_scratch_locked(need, stream, &ws)) return rc;
+            // A stream under graph capture cannot allocate: a key split whose
+            // partial rows do not fit the stream's library scratch is dropped
+            // (the split only spreads the work; the result is the same).
+            if (r.key_splits > 1 && library_scratch_bytes_locked(stream) < need && stream_capturing(stream)) {
+                no_key_split(p, r);
+                need = workspace_bytes_for(p, r);
+            }
+            if (need > 0)
+                if (int rc = library_scratch_locked(need, stream, &ws)) return rc;
         } else if (workspace_bytes < need) {
             return set_error(OFH_ERROR_WORKSPACE_TOO_SMALL,
                              "workspace too small: need " + std::to_string(need) + " bytes");
@@ -368,9 +450,12 @@ int fwd_impl(const ofh_attention_params* p, const void* q, const void* k, const 
         char* base = static_cast<char*>(ws) + round256(list_bytes(r));
         a.part_o = reinterpret_cast<float*>(base);
         a.part_ml = reinterpret_cast<float*>(base + round256(partial_rows(p, r) * p->value_dim * 4));
+        if (merge_in_launch(p, r))
+            if (int rc = split_counters_for(stream, noalloc, &a.split_counters)) return rc;
     }
     OFH_HIP_CHECK(ofh::launch_flash_mfma(a, p->dtype, r.general_mod, stream));
-    if (r.key_splits > 1) OFH_HIP_CHECK(ofh::launch_combine_splits(a, stream));
+    if (r.key_splits > 1 && a.split_counters == nullptr)
+        OFH_HIP_CHECK(ofh::launch_combine_splits(a, p->dtype, stream));
     return OFH_SUCCESS;
 }
 
@@ -449,7 +534,7 @@ int ofh_attention_fwd_noalloc(const ofh_attention_params* p, const void* q, cons
     void* ws = nullptr;
     if (need > 0) OFH_HIP_CHECK(ofh::noalloc_scratch(&ws));
     return fwd_impl(p, q, k, v, out, ws, need > 0 ? ofh::kNoAllocScratchBytes : 0,
-                    static_cast<hipStream_t>(stream));
+                    static_cast<hipStream_t>(stream), true);
 }
 
 int ofh_attention_fwd_host(const ofh_attention_params* p, const float* q, const float* k,
@@ -555,6 +640,7 @@ int ofh_attention_launch_info(const ofh_attention_params* p, ofh_launch_info* in
         info->workgroups = (int64_t)p->batch * p->heads * (r.paired ? (r.num_q_tiles + 1) / 2 : r.num_q_tiles) *
                            r.key_splits;
         info->key_splits = r.key_splits;
+        info->merge_in_launch = merge_in_launch(p, r) ? 1 : 0;
         name = ofh::flash_mfma_kernel_name(p->dtype, (int)p->head_dim, r.general_mod, r.tile_list);
     } else {
         info->block_m = 1;

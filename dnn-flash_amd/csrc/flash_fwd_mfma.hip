@@ -28,6 +28,9 @@
 // next MFMA wants in a lane (k-slots 8g..8g+7 of a 16-wide chunk), and what
 // a 16-byte store of the output wants.
 
+#include <map>
+#include <mutex>
+
 #include "ofh_kernels.h"
 
 namespace ofh {
@@ -42,6 +45,14 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
+
+// s_waitcnt vmcnt(0): every vector-memory load issued so far has returned
+// (and every store has completed: gfx9 counts both in vmcnt). Issued once
+// before the tile loop, it tells the compiler's wait-count tracking that the
+// Q fragments are resident on every path into the loop; without it the loop
+// waits on them (and so on every load issued after them, i.e. the K/V
+// prefetch) at each use.
+__device__ __forceinline__ void wait_vm_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 __device__ __forceinline__ int kappa(int r) {
     return ((r >> 4) << 4) | (((r >> 2) & 1) << 3) | (((r >> 3) & 1) << 2) | (r & 3);
@@ -204,6 +215,185 @@ __device__ __forceinline__ float online_softmax_tile(const FwdArgs& a, f32x16 (&
 }
 
 // ---------------------------------------------------------------------------
+// Key split (FwdArgs::num_splits > 1). Query tile qt has steps(qt) K/V tile
+// steps; splits [0, active(qt)) of it run, split s over steps
+// [s*split_tiles, (s+1)*split_tiles). With one active split, split 0 writes O
+// directly. Otherwise every active split writes its unnormalised partial rows
+// (O_s, m_s, l_s) and the rows are merged with the log-sum-exp rule of
+// attention.cpp:661-674 applied across splits:
+//   m* = max_s m_s,  O = sum_s 2^(m_s - m*) O_s / sum_s 2^(m_s - m*) l_s.
+// Rows that saw no valid key in any split (l = 0) are written as 0.
+
+__device__ __forceinline__ int split_active(const FwdArgs& a, int steps) {
+    return max(1, min(a.num_splits, (steps + a.split_tiles - 1) / a.split_tiles));
+}
+
+// Folds partial (m2, l2, o2) into (m, l, o); maxima in log2 units.
+__device__ __forceinline__ void lse_fold(float& m, float& l, f32x4& o, float m2, float l2, f32x4 o2) {
+    const float mg = fmaxf(m, m2);
+    const float mu = mg == kNegInf ? 0.0f : mg;
+    const float w1 = __builtin_amdgcn_exp2f(m - mu), w2 = __builtin_amdgcn_exp2f(m2 - mu);  // 0 for -inf
+    l = l * w1 + l2 * w2;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) o[t] = o[t] * w1 + o2[t] * w2;
+    m = mg;
+}
+
+// Partial rows merged inside the launch that writes them (split_counters set)
+// are stored and loaded with agent-scope atomics: each access is coherent
+// across the XCDs' L2 caches by itself, so no L2 writeback or invalidation
+// (an agent-scope fence) is needed, which would cost every other workgroup on
+// the XCD its cached K/V tiles. Partial rows merged by a second launch use
+// plain accesses (the launch boundary makes them visible).
+__device__ __forceinline__ void put_partial(float* p, float v, bool coherent) {
+    if (coherent) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *p = v;
+}
+__device__ __forceinline__ void put_partial4(float* p, f32x4 v, bool coherent) {
+    if (coherent) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) __hip_atomic_store(p + t, v[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        *(f32x4*)p = v;
+    }
+}
+template <bool COHERENT>
+__device__ __forceinline__ float get_partial(const float* p) {
+    if (COHERENT) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return *p;
+}
+template <bool COHERENT>
+__device__ __forceinline__ f32x4 get_partial4(const float* p) {
+    if (COHERENT) {
+        f32x4 v;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] = __hip_atomic_load(p + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return v;
+    }
+    return *(const f32x4*)p;
+}
+
+// Merges columns [4c, 4c+4) of partial row prow over splits s0, s0+sstep, ...
+// below `active`, four splits per group so that their loads are in flight
+// together; the running max is raised per group.
+template <bool COHERENT>
+__device__ __forceinline__ void merge_partials(const FwdArgs& a, int64_t prow, int c, int s0, int sstep,
+                                               int active, float& m, float& l, f32x4& acc) {
+    const int64_t stride = (int64_t)a.B * a.H * a.M;
+    constexpr int G = 4;
+    for (int s = s0; s < active; s += G * sstep) {
+        float ms[G], ls[G];
+        f32x4 os[G];
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const bool ok = s + j * sstep < active;
+            const int64_t r = (int64_t)(ok ? s + j * sstep : s) * stride + prow;
+            // (plain float loads: element 1 of a loaded u32x2 passed through
+            // __builtin_bit_cast was read as element 0 by this compiler)
+            ms[j] = ok ? get_partial<COHERENT>(a.part_ml + 2 * r) : kNegInf;
+            ls[j] = get_partial<COHERENT>(a.part_ml + 2 * r + 1);
+            os[j] = get_partial4<COHERENT>(a.part_o + r * a.Dv + 4 * c);
+        }
+        float mg = m;
+#pragma unroll
+        for (int j = 0; j < G; ++j) mg = fmaxf(mg, ms[j]);
+        const float mu = mg == kNegInf ? 0.0f : mg;
+        const float keep = __builtin_amdgcn_exp2f(m - mu);  // 0 while m is -inf
+        l *= keep;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] *= keep;
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const float w = __builtin_amdgcn_exp2f(ms[j] - mu);  // 0 for splits past `active`
+            l += w * ls[j];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[t] += w * os[j][t];
+        }
+        m = mg;
+    }
+}
+
+// Writes columns [4c, 4c+4) of O row `row` of head bh, normalised by l.
+template <typename T>
+__device__ __forceinline__ void store_merged(const FwdArgs& a, int bh, int row, int c, float l, f32x4 acc) {
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int64_t off = b * a.o_sb + h * a.o_sh + (int64_t)row * a.o_sm + 4 * c;
+    if (sizeof(T) == 4 || a.out_f32) {
+        *(f32x4*)((float*)a.o + off) = acc * inv;
+    } else if constexpr (sizeof(T) == 2) {
+        typedef T v4 __attribute__((ext_vector_type(4)));
+        v4 val;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) val[t] = (T)(acc[t] * inv);
+        *(v4*)((T*)a.o + off) = val;
+    }
+}
+
+// Counts this workgroup in its query tile's arrival counter once the partial
+// rows of every thread are stored (agent-scope atomic stores, complete when
+// vmcnt reaches 0); true in the workgroup that arrives last, to which the
+// partial rows of all splits of the tile are then visible through agent-scope
+// atomic loads. That workgroup sets the counter back to zero for the next
+// call on the stream. Every thread calls it; `flag` is one int of LDS.
+__device__ __forceinline__ bool split_arrive(unsigned* ctr, int active, int* flag) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the partial-row stores stay above the wait
+    wait_vm_loads();                          // vmcnt(0): this thread's stores have completed
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = prev + 1 == (unsigned)active;
+        if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = last ? 1 : 0;
+    }
+    __syncthreads();
+    return *flag != 0;
+}
+
+// Merge of the `rows` rows from q0 of head bh by one workgroup of NTHREADS
+// threads: a thread per (row, 4-column chunk); when there are fewer such
+// items than threads (few rows), the splits are shared out over groups of
+// threads whose results are folded through `red` (6 * NTHREADS floats of LDS).
+template <typename T, int NTHREADS>
+__device__ void merge_split_rows(const FwdArgs& a, int bh, int q0, int rows, int active, float* red) {
+    const int chunks = a.Dv >> 2;
+    const int items = rows * chunks;
+    const int t = threadIdx.x;
+    if (items >= NTHREADS) {
+        for (int item = t; item < items; item += NTHREADS) {
+            const int rr = item / chunks, c = item - rr * chunks;
+            float m = kNegInf, l = 0.0f;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            merge_partials<true>(a, (int64_t)bh * a.M + q0 + rr, c, 0, 1, active, m, l, acc);
+            store_merged<T>(a, bh, q0 + rr, c, l, acc);
+        }
+        return;
+    }
+    const int groups = min(active, NTHREADS / items);
+    const int item = t % items, grp = t / items;
+    const bool mine = grp < groups;
+    const int rr = item / chunks, c = item - rr * chunks;
+    float m = kNegInf, l = 0.0f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (mine) merge_partials<true>(a, (int64_t)bh * a.M + q0 + rr, c, grp, groups, active, m, l, acc);
+    if (mine && grp > 0) {
+        float* e = red + 6 * (grp * items + item);
+        e[0] = m;
+        e[1] = l;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) e[2 + j] = acc[j];
+    }
+    __syncthreads();
+    if (grp == 0) {
+        for (int j = 1; j < groups; ++j) {
+            const float* e = red + 6 * (j * items + item);
+            lse_fold(m, l, acc, e[0], e[1], f32x4{e[2], e[3], e[4], e[5]});
+        }
+        store_merged<T>(a, bh, q0 + rr, c, l, acc);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // bf16 / fp16 inputs, fp32 accumulate: v_mfma_f32_32x32x16_{bf16,f16}.
 //
 // Every wavefront owns 32 query rows. K/V tiles are staged one tile ahead
@@ -247,12 +437,6 @@ typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 // any mix of ALiBi / dense bias / soft-cap selected per call.
 enum ScoreMod { MOD_PLAIN = 0, MOD_GENERAL = 1 };
 
-// s_waitcnt vmcnt(0): every vector-memory load issued so far has returned.
-// Issued once before the tile loop, it tells the compiler's wait-count
-// tracking that the Q fragments are resident on every path into the loop;
-// without it the loop waits on them (and so on every load issued after
-// them, i.e. the K/V prefetch) at each use.
-__device__ __forceinline__ void wait_vm_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // One 16-byte global -> LDS copy per lane (lane L writes lds + 16 L; lds is
 // wave-uniform). Written as assembly so that the compiler does not make LDS
@@ -317,6 +501,7 @@ __device__ __forceinline__ constexpr int tile_pos(int sb, int e) { return 32 * s
 // block-mask list (LIST) the list entry (key tile + per-slice bits).
 template <typename T, int D, int MOD, bool LIST, int NTHREADS, int BN_, int SB = 1>
 struct Wave32 {
+    using T_ = T;
     using M16 = Mfma16<T>;
     using v8 = typename M16::v8;
     // K/V staged by global -> LDS copies in every kernel without a block-mask
@@ -671,6 +856,33 @@ struct Wave32 {
         l_run += lsum;
     }
 
+    // Key split: the unnormalised rows and (m, l) of split `split`.
+    __device__ __forceinline__ void store_partial(int split) {
+        const float l_tot = l_run + __shfl_xor(l_run, 32);
+        if (my_q >= a.M) return;
+        const int64_t prow = ((int64_t)split * a.B * a.H + (int64_t)b * a.H + h) * a.M + my_q;
+        float* po = a.part_o + prow * D + 8 * g;
+        const bool coh = a.split_counters != nullptr;
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) {
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+                f32x4 lo, hi;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    lo[t] = o[db][8 * cc + t];
+                    hi[t] = o[db][8 * cc + 4 + t];
+                }
+                put_partial4(po + 32 * db + 16 * cc, lo, coh);
+                put_partial4(po + 32 * db + 16 * cc + 4, hi, coh);
+            }
+        }
+        if (g == 0) {
+            put_partial(a.part_ml + 2 * prow, m_run, coh);
+            put_partial(a.part_ml + 2 * prow + 1, l_tot, coh);
+        }
+    }
+
     // Normalise and store; rows that saw no valid key have l = 0 and are written as 0.
     __device__ __forceinline__ void store_output() {
         const float l_tot = l_run + __shfl_xor(l_run, 32);
@@ -728,38 +940,61 @@ __device__ __forceinline__ void tile_range(const FwdArgs& a, int qt, int block_m
 // start of step it and are awaited before the barrier that ends it, so their
 // latency hides behind a whole step. With a list, entries are loaded two
 // steps ahead of their use.
-template <typename T, int D, int MOD, bool LIST, int NWAVES, int BN, int SB = 1>
-__device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* smem, int bh, int qt) {
+// End of a query tile (or of its key split `split` of `active`): O, or the
+// partial rows followed by the merge in the split workgroup that arrives last.
+template <typename W, int NTHREADS, bool SPLIT>
+__device__ __forceinline__ void finish_qtile(const FwdArgs& a, W& w, unsigned char* smem, int bh, int qt,
+                                             int q0, int block_m, int split, int active) {
+    if (!SPLIT || active <= 1) {
+        w.store_output();
+        return;
+    }
+    w.store_partial(split);
+    if (a.split_counters == nullptr) return;  // merged by combine_splits_kernel
+    __syncthreads();                          // LDS below is reused
+    int* flag = (int*)(smem + 24 * NTHREADS);
+    if (split_arrive(a.split_counters + (int64_t)bh * a.num_q_tiles + qt, active, flag))
+        merge_split_rows<typename W::T_, NTHREADS>(a, bh, q0, min(block_m, a.M - q0), active, (float*)smem);
+}
+
+template <typename T, int D, int MOD, bool LIST, int NWAVES, int BN, int SB, bool SPLIT>
+__device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* smem, int bh, int qt,
+                                               int split = 0) {
     constexpr int NTHREADS = NWAVES * 64;
     constexpr int BLOCK_M = NWAVES * kQueriesPerWave;
     static_assert(!LIST || NWAVES <= kListSlices, "list entries carry one bit per wavefront");
     using W = Wave32<T, D, MOD, LIST, NTHREADS, BN, SB>;
     using L = typename W::L;
+    static_assert(2 * L::STAGE >= 24 * NTHREADS + 4, "split merge scratch fits in the LDS stages");
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    W w(a, smem, bh, qt * BLOCK_M, wave);
+    const int q0 = qt * BLOCK_M;
     if constexpr (!LIST) {
         // SB compute steps of BN keys per staged tile of SB*BN keys (one
         // barrier per staged tile); no list. Tile
         // st+1 is copied global -> LDS (no registers) into the free stage at
         // the start of step st and awaited before the barrier that ends it.
         static_assert(!LIST, "LDS copies: no list");
-        const int q0 = qt * BLOCK_M;
         const int kend = a.causal ? min(a.N, q0 + BLOCK_M) : a.N;
         const int nst = (kend + W::SN - 1) / W::SN;      // staged tiles
-        if (nst == 0) {  // uniform over the workgroup
-            w.store_output();
+        const int active = SPLIT ? split_active(a, nst) : 1;
+        if (split >= active) return;                     // uniform over the workgroup
+        const int st0 = SPLIT ? split * a.split_tiles : 0;
+        const int st1 = SPLIT ? min(nst, st0 + a.split_tiles) : nst;
+        W w(a, smem, bh, q0, wave);
+        if (st0 >= st1) {  // uniform over the workgroup
+            finish_qtile<W, NTHREADS, SPLIT>(a, w, smem, bh, qt, q0, BLOCK_M, split, active);
             return;
         }
         // (returning early keeps every path into the loop through the wait
         // below, so the compiler sees the Q fragments resident in the loop)
-        w.copy_tile(0, 0);
+        w.copy_tile(st0, 0);
         wait_vm_loads();
-        w.zero_tail(0, 0);
+        w.zero_tail(st0, 0);
         __syncthreads();
-        for (int st = 0; st < nst; ++st) {
-            const int stage = (st & 1) * L::STAGE;
-            const int nstage = ((st + 1) & 1) * L::STAGE;
-            if (st + 1 < nst) w.copy_tile(st + 1, nstage);
+        for (int st = st0; st < st1; ++st) {
+            const int stage = ((st - st0) & 1) * L::STAGE;
+            const int nstage = ((st - st0 + 1) & 1) * L::STAGE;
+            if (st + 1 < st1) w.copy_tile(st + 1, nstage);
 #pragma unroll
             for (int j = 0; j < SB; ++j) {
                 const int e = st * SB + j;               // BN-key compute tile
@@ -779,30 +1014,38 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
                 }
             }
             wait_vm_loads();
-            if (st + 1 < nst) w.zero_tail(st + 1, nstage);
+            if (st + 1 < st1) w.zero_tail(st + 1, nstage);
             __syncthreads();
         }
-        w.store_output();
+        finish_qtile<W, NTHREADS, SPLIT>(a, w, smem, bh, qt, q0, BLOCK_M, split, active);
         return;
     }
-    tile_range(a, qt, BLOCK_M, BN, w.ntiles, w.list);
-    const int ntiles = w.ntiles;
+    int ntiles;
+    const int* list;
+    tile_range(a, qt, BLOCK_M, BN, ntiles, list);
+    const int active = SPLIT ? split_active(a, ntiles) : 1;
+    if (split >= active) return;  // uniform over the workgroup
+    const int it0 = SPLIT ? split * a.split_tiles : 0;
+    const int it1 = SPLIT ? min(ntiles, it0 + a.split_tiles) : ntiles;
+    W w(a, smem, bh, q0, wave);
+    w.ntiles = ntiles;
+    w.list = list;
     // entry it+1 is copied during step it
-    if (ntiles == 0) {
-        w.store_output();
+    if (it0 >= it1) {
+        finish_qtile<W, NTHREADS, SPLIT>(a, w, smem, bh, qt, q0, BLOCK_M, split, active);
         return;
     }
-    int e_cur = w.entry(0);
-    int e_nxt = ntiles > 1 ? w.entry(1) : 0;
+    int e_cur = w.entry(it0);
+    int e_nxt = it0 + 1 < it1 ? w.entry(it0 + 1) : 0;
     w.copy_tile(w.tile_of(e_cur), 0);
     wait_vm_loads();
     w.zero_tail(w.tile_of(e_cur), 0);
     __syncthreads();
-    for (int it = 0; it < ntiles; ++it) {
-        const int stage = (it & 1) * L::STAGE;
-        const int nstage = ((it + 1) & 1) * L::STAGE;
-        if (it + 1 < ntiles) w.copy_tile(w.tile_of(e_nxt), nstage);
-        const int e_nn = it + 2 < ntiles ? w.entry(it + 2) : 0;
+    for (int it = it0; it < it1; ++it) {
+        const int stage = ((it - it0) & 1) * L::STAGE;
+        const int nstage = ((it - it0 + 1) & 1) * L::STAGE;
+        if (it + 1 < it1) w.copy_tile(w.tile_of(e_nxt), nstage);
+        const int e_nn = it + 2 < it1 ? w.entry(it + 2) : 0;
         if (w.tile_active(e_cur)) {
             if (MOD == MOD_PLAIN) __builtin_amdgcn_s_setprio(1);
             w.qk(stage);
@@ -813,12 +1056,12 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
             if (MOD == MOD_PLAIN) __builtin_amdgcn_s_setprio(0);
         }
         wait_vm_loads();
-        if (it + 1 < ntiles) w.zero_tail(w.tile_of(e_nxt), nstage);
+        if (it + 1 < it1) w.zero_tail(w.tile_of(e_nxt), nstage);
         __syncthreads();
         e_cur = e_nxt;
         e_nxt = e_nn;
     }
-    w.store_output();
+    finish_qtile<W, NTHREADS, SPLIT>(a, w, smem, bh, qt, q0, BLOCK_M, split, active);
 }
 
 template <typename T, int D, int MOD, bool LIST, int NWAVES, bool PAIRED, int BN = kBlockN16, int SB = 1>
@@ -826,11 +1069,19 @@ __global__ __launch_bounds__(NWAVES * 64, 8 / NWAVES) void flash_fwd_lockstep_ke
     using L = TileLayout<D, BN * SB>;
     __shared__ __attribute__((aligned(16))) unsigned char smem[2 * L::STAGE];
     int bh, qts[2];
+    if (!PAIRED) {  // key split s: workgroups [s * tiles, (s+1) * tiles)
+        const int tiles = a.B * a.H * a.num_q_tiles;
+        const int split = (int)blockIdx.x / tiles;
+        map_work((int)blockIdx.x - split * tiles, a.B * a.H, a.num_q_tiles, a.causal, bh, qts[0]);
+        lockstep_qtile<T, D, MOD, LIST, NWAVES, BN, SB, true>(a, smem, bh, qts[0], split);
+        return;
+    }
+    // (paired query tiles are never split)
     const int n = work_tiles(a, PAIRED, bh, qts);
-    lockstep_qtile<T, D, MOD, LIST, NWAVES, BN, SB>(a, smem, bh, qts[0]);
+    lockstep_qtile<T, D, MOD, LIST, NWAVES, BN, SB, false>(a, smem, bh, qts[0]);
     if (n > 1) {
         __syncthreads();  // LDS stages are reused
-        lockstep_qtile<T, D, MOD, LIST, NWAVES, BN, SB>(a, smem, bh, qts[1]);
+        lockstep_qtile<T, D, MOD, LIST, NWAVES, BN, SB, false>(a, smem, bh, qts[1]);
     }
 }
 
@@ -900,9 +1151,10 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a)
         ntiles = (kend + BN - 1) / BN;
     }
     // tile steps [it0, it1) of this workgroup's key split
+    const int active = split_active(a, ntiles);
+    if (split >= active) return;  // uniform over the workgroup
     const int it0 = split * a.split_tiles;
     const int it1 = min(ntiles, it0 + a.split_tiles);
-    if (a.num_splits > 1 && it0 >= it1) return;  // no key tile in this split (the combine skips it)
 
     f32x4 kreg[CPT], vreg[CPT];
     auto load_tile = [&](int kt) {
@@ -1006,11 +1258,12 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a)
     }
 
     const float l_tot = l_run + __shfl_xor(l_run, 32);
-    if (a.num_splits > 1) {
-        // partial row: unnormalised O and (m, l); the combine merges the splits
+    if (active > 1) {
+        // partial row: unnormalised O and (m, l), merged by the last split to arrive
         if (my_q < a.M) {
             const int64_t prow = ((int64_t)split * a.B * a.H + bh) * a.M + my_q;
             float* po = a.part_o + prow * D + 4 * g;
+            const bool coh = a.split_counters != nullptr;
 #pragma unroll
             for (int db = 0; db < D / 32; ++db) {
 #pragma unroll
@@ -1018,14 +1271,20 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a)
                     f32x4 val;
 #pragma unroll
                     for (int j = 0; j < 4; ++j) val[j] = o[db][4 * i + j];
-                    *(f32x4*)(po + 32 * db + 8 * i) = val;
+                    put_partial4(po + 32 * db + 8 * i, val, coh);
                 }
             }
             if (g == 0) {
-                a.part_ml[2 * prow] = m_run;
-                a.part_ml[2 * prow + 1] = l_tot;
+                put_partial(a.part_ml + 2 * prow, m_run, coh);
+                put_partial(a.part_ml + 2 * prow + 1, l_tot, coh);
             }
         }
+        if (a.split_counters == nullptr) return;  // merged by combine_splits_kernel
+        __syncthreads();                          // LDS below is reused
+        static_assert(2 * STAGE * 4 >= 24 * kThreads32 + 4, "split merge scratch fits in the LDS stages");
+        int* flag = (int*)(lds + 6 * kThreads32);
+        if (split_arrive(a.split_counters + (int64_t)bh * a.num_q_tiles + qt, active, flag))
+            merge_split_rows<float, kThreads32>(a, bh, q0, min(kBlockM32, a.M - q0), active, lds);
         return;
     }
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
@@ -1044,22 +1303,21 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a)
     }
 }
 
-// Merge of key-split partial rows: one thread per (head, row, 4 columns).
-// For row i of query tile qt, splits [0, ceil(steps(qt) / split_tiles)) ran;
-// with m* = max_s m_s: O = sum_s 2^(m_s - m*) O_s / sum_s 2^(m_s - m*) l_s, the
-// log-sum-exp merge of attention.cpp:661-674 applied across splits. Rows with
-// no valid key in any split (l = 0) are written as 0.
-template <typename TO>
-__global__ __launch_bounds__(256) void combine_splits_kernel(FwdArgs a) {
-    const int chunks = a.Dv / 4;
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t total = (int64_t)a.B * a.H * a.M * chunks;
-    if (idx >= total) return;
-    const int c = (int)(idx % chunks);
-    const int64_t t = idx / chunks;
-    const int row = (int)(t % a.M);
-    const int bh = (int)(t / a.M);
-    const int qt = row / a.split_bm;
+// Merge of key-split partial rows in a launch of its own (no arrival
+// counters). A workgroup merges `rows` consecutive rows of one head (a power
+// of two, so they lie in one query tile): thread t takes (row, 4-column chunk)
+// item t % (rows * chunks) and the splits grp, grp + groups, ... with
+// grp = t / (rows * chunks), so that a row's splits are read by `groups`
+// threads at once; the groups' results are folded through LDS. T is the
+// input type (the output type unless out_f32).
+template <typename T>
+__global__ __launch_bounds__(256) void combine_splits_kernel(FwdArgs a, int rows, int groups) {
+    __shared__ float red[6 * 256];
+    const int chunks = a.Dv >> 2;
+    const int per_head = (a.M + rows - 1) / rows;
+    const int bh = (int)blockIdx.x / per_head;
+    const int row0 = ((int)blockIdx.x - bh * per_head) * rows;
+    const int qt = row0 / a.split_bm;
     int steps;
     if (a.tile_counts != nullptr) {
         steps = a.tile_counts[qt];
@@ -1067,46 +1325,34 @@ __global__ __launch_bounds__(256) void combine_splits_kernel(FwdArgs a) {
         const int kend = a.causal ? min(a.N, (qt + 1) * a.split_bm) : a.N;
         steps = (kend + a.split_bn - 1) / a.split_bn;
     }
-    const int active = min(a.num_splits, (steps + a.split_tiles - 1) / a.split_tiles);
-    const int64_t stride = (int64_t)a.B * a.H * a.M;
-    const int64_t prow = (int64_t)bh * a.M + row;
-    // One pass in groups of four splits: the loads of a group are independent,
-    // so they are in flight together; the running max is raised per group.
-    constexpr int G = 4;
+    const int active = split_active(a, steps);
+    if (active <= 1) return;  // split 0 wrote these rows (uniform over the workgroup)
+    const int items = rows * chunks;  // items * groups <= 256
+    const int t = threadIdx.x;
+    const int item = t % items, grp = t / items;
+    const int rr = item / chunks, c = item - rr * chunks;
+    const int row = row0 + rr;
+    const int ng = min(groups, active);
+    const bool mine = grp < ng && row < a.M;
     float m = kNegInf, l = 0.0f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < active; s0 += G) {
-        float ms[G], ls[G];
-        f32x4 os[G];
+    if (mine) merge_partials<false>(a, (int64_t)bh * a.M + row, c, grp, ng, active, m, l, acc);
+    if (ng > 1) {
+        if (mine && grp > 0) {
+            float* e = red + 6 * t;
+            e[0] = m;
+            e[1] = l;
 #pragma unroll
-        for (int j = 0; j < G; ++j) {
-            const int64_t r = (int64_t)min(s0 + j, active - 1) * stride + prow;
-            ms[j] = s0 + j < active ? a.part_ml[2 * r] : kNegInf;
-            ls[j] = a.part_ml[2 * r + 1];
-            os[j] = *(const f32x4*)(a.part_o + r * a.Dv + 4 * c);
+            for (int j = 0; j < 4; ++j) e[2 + j] = acc[j];
         }
-        float mg = m;
-#pragma unroll
-        for (int j = 0; j < G; ++j) mg = fmaxf(mg, ms[j]);
-        const float mu = mg == kNegInf ? 0.0f : mg;
-        const float keep = __builtin_amdgcn_exp2f(m - mu);  // 0 while m is -inf
-        l *= keep;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) acc[t] *= keep;
-#pragma unroll
-        for (int j = 0; j < G; ++j) {
-            const float w = __builtin_amdgcn_exp2f(ms[j] - mu);  // 0 for splits past `active`
-            l += w * ls[j];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) acc[t] += w * os[j][t];
-        }
-        m = mg;
+        __syncthreads();
+        if (mine && grp == 0)
+            for (int j = 1; j < ng; ++j) {
+                const float* e = red + 6 * (j * items + item);
+                lse_fold(m, l, acc, e[0], e[1], f32x4{e[2], e[3], e[4], e[5]});
+            }
     }
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    const int b = bh / a.H, h = bh - b * a.H;
-    TO* orow = (TO*)a.o + b * a.o_sb + h * a.o_sh + (int64_t)row * a.o_sm + 4 * c;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) orow[j] = (TO)(acc[j] * inv);
+    if (mine && grp == 0) store_merged<T>(a, bh, row, c, l, acc);
 }
 
 template <typename K>
@@ -1141,7 +1387,7 @@ static int block_n16(bool general_mod, bool tile_list) {
 template <typename T, int D>
 static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
     const bool list = a.tile_counts != nullptr;
-    const bool paired = pairs_causal_tiles(a.causal != 0, list);
+    const bool paired = pairs_causal_tiles(a.causal != 0, list) && a.num_splits == 1;
     if (list)
         return general_mod ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, true, 4, false>, 256, a, s)
                            : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, true, 4, false>, 256, a, s);
@@ -1173,13 +1419,48 @@ hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipS
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_combine_splits(const FwdArgs& a, hipStream_t s) {
-    const int64_t total = (int64_t)a.B * a.H * a.M * (a.Dv / 4);
-    if (total <= 0) return hipSuccess;
-    const dim3 grid((unsigned)((total + 255) / 256));
-    if (a.out_f32) hipLaunchKernelGGL(combine_splits_kernel<float>, grid, dim3(256), 0, s, a);
-    else return hipErrorInvalidValue;  // the key split is used by the fp32 kernel only
+hipError_t launch_combine_splits(const FwdArgs& a, int dtype, hipStream_t s) {
+    const int chunks = a.Dv / 4;
+    if (a.B * a.H * a.M <= 0 || chunks <= 0 || chunks > 256 || a.split_bm <= 0) return hipErrorInvalidValue;
+    // splits per row read in parallel: up to 8 groups (two rounds of four
+    // loads per thread for 64 splits); rows per workgroup: a power of two
+    // dividing the query tile, with rows * chunks * groups <= 256
+    int groups = 1;
+    while (groups < 8 && groups < a.num_splits && 2 * groups * chunks <= 256) groups *= 2;
+    int rows = 1;
+    while (2 * rows * chunks * groups <= 256 && 2 * rows <= a.split_bm && a.split_bm % (2 * rows) == 0) rows *= 2;
+    const int64_t nblk = (int64_t)a.B * a.H * ((a.M + rows - 1) / rows);
+    if (nblk > 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)nblk);
+    if (dtype == DT_F32 || a.out_f32) hipLaunchKernelGGL(combine_splits_kernel<float>, grid, dim3(256), 0, s, a, rows, groups);
+    else if (dtype == DT_BF16) hipLaunchKernelGGL(combine_splits_kernel<__bf16>, grid, dim3(256), 0, s, a, rows, groups);
+    else if (dtype == DT_F16) hipLaunchKernelGGL(combine_splits_kernel<_Float16>, grid, dim3(256), 0, s, a, rows, groups);
+    else return hipErrorInvalidValue;
     return hipGetLastError();
+}
+
+namespace {
+// Arrival counters of the single-launch key-split merge (see FwdArgs).
+static __device__ __align__(256) unsigned split_counters[kSplitCounterSlots * kMaxSplitTiles];
+std::mutex g_counter_mu;
+std::map<int, unsigned*> g_counter_addr;  // device -> address of its copy of split_counters
+}  // namespace
+
+hipError_t split_counter_slot(int slot, unsigned** ptr) {
+    if (slot < 0 || slot >= kSplitCounterSlots) return hipErrorInvalidValue;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(g_counter_mu);
+    auto it = g_counter_addr.find(dev);
+    if (it == g_counter_addr.end()) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(split_counters));
+        if (e != hipSuccess) return e;
+        it = g_counter_addr.emplace(dev, static_cast<unsigned*>(p)).first;
+    }
+    *ptr = it->second + (size_t)slot * kMaxSplitTiles;
+    return hipSuccess;
 }
 
 const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile_list) {

@@ -53,15 +53,31 @@ struct FwdArgs {
     float inv_softcap;
     int out_f32;        // 1: O is fp32, else O has the input dtype
     // Key split: workgroup s of a query tile runs its K/V tile steps
-    // [s*split_tiles, (s+1)*split_tiles) and, when num_splits > 1, writes the
-    // unnormalised O rows and (m, l) per row to part_o / part_ml instead of O;
-    // combine_splits merges them. num_splits == 1: one workgroup per query tile.
+    // [s*split_tiles, (s+1)*split_tiles). A query tile with steps(qt) steps has
+    // active(qt) = max(1, min(num_splits, ceil(steps(qt) / split_tiles)))
+    // splits; with one, split 0 writes O itself. Otherwise every active split
+    // writes its unnormalised O rows and (m, l) per row to part_o / part_ml,
+    // and the rows are merged into O: by the split workgroup that arrives last
+    // (counted in split_counters, which it leaves at zero), or, with
+    // split_counters null, by combine_splits_kernel in a second launch.
+    // num_splits == 1: one workgroup per query tile.
     int num_splits;
     int split_tiles;
-    int split_bm, split_bn;  // query rows per query tile and keys per K/V tile of the split kernel
+    int split_bm, split_bn;  // query rows per query tile and keys per K/V tile step (every call)
     float* part_o;           // [num_splits][B*H][M][Dv] fp32
     float* part_ml;          // [num_splits][B*H][M][2] fp32: running max (log2 units), row sum
+    unsigned* split_counters;  // [B*H*num_q_tiles] arrival counters, zero between calls, or null
 };
+
+// Single-launch key-split merge: arrival counters live in a static device
+// array of kSplitCounterSlots slots of kMaxSplitTiles counters per GPU. A slot
+// is used by one stream at a time (calls on a stream run in order); every call
+// leaves the counters it used at zero, the state the code object loads with.
+constexpr int kSplitCounterSlots = 64;
+constexpr int kMaxSplitTiles = 1024;
+// Device address of counter slot `slot` on the current device (looked up once
+// per device, then cached).
+hipError_t split_counter_slot(int slot, unsigned** ptr);
 
 // Block-mask tile list entry: the key tile index and, for each 32-row slice
 // w of the query tile (one wavefront each, at most kListSlices), bit w: the
@@ -107,8 +123,9 @@ struct QkScoreArgs {
 hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipStream_t s);
 hipError_t launch_rowwise(const FwdArgs& a, int dtype, hipStream_t s);
 hipError_t launch_tile_lists(const TileListArgs& a, hipStream_t s);
-// Merge of the key-split partial rows into O (num_splits > 1).
-hipError_t launch_combine_splits(const FwdArgs& a, hipStream_t s);
+// Merge of the key-split partial rows into O in a second launch (num_splits > 1,
+// split_counters null); dtype is the input type.
+hipError_t launch_combine_splits(const FwdArgs& a, int dtype, hipStream_t s);
 hipError_t launch_qk_score(const QkScoreArgs& a, int dtype, hipStream_t s);
 // Matrix-core score kernel for bf16/fp16 with unit k-strides and 16-byte rows.
 bool qk_score_mfma_supported(const QkScoreArgs& a, int dtype);

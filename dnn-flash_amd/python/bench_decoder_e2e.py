@@ -82,8 +82,14 @@ def materialized_attention(torch, q, k, v, *, causal: bool):
     return torch.matmul(probs, v)
 
 
-def flash_attention(q, k, v, *, causal: bool):
-    return F.onednn_flash_attention(q, k, v, causal=causal)
+def flash_attention(q, k, v, *, causal: bool, workspace=None):
+    """The library's attention; with `workspace` (sized by
+    ofh_attention_workspace_bytes) the call allocates nothing, as graph
+    capture requires."""
+    if workspace is None:
+        return F.onednn_flash_attention(q, k, v, causal=causal)
+    return F.attention_fwd(q, k, v, scale=1.0 / math.sqrt(q.shape[3]), causal=causal,
+                           workspace=workspace)
 
 
 def make_weights(torch, cfg: BenchConfig, dtype):
@@ -156,7 +162,10 @@ def run_one(torch, cfg: BenchConfig, *, graph: bool) -> dict[str, Any]:
     x = stable_values(torch, (B, S, cfg.embed_dim), seed=14, dtype=dtype)
     w = make_weights(torch, cfg, dtype)
     mat = lambda q_, k_, v_: materialized_attention(torch, q_, k_, v_, causal=cfg.causal)  # noqa: E731
-    fla = lambda q_, k_, v_: flash_attention(q_, k_, v_, causal=cfg.causal)  # noqa: E731
+    # a workspace sized once up front: no allocation inside the call (graph capture)
+    ws = torch.empty(max(1, F.workspace_bytes(F.make_params(
+        B, H, S, S, D, dtype=F.dtype_code(dtype), causal=cfg.causal))), dtype=torch.uint8, device="cuda")
+    fla = lambda q_, k_, v_: flash_attention(q_, k_, v_, causal=cfg.causal, workspace=ws)  # noqa: E731
 
     ref_attn, our_attn = mat(q, k, v), fla(q, k, v)
     ref_dec, our_dec = decoder_block(torch, x, w, cfg, mat), decoder_block(torch, x, w, cfg, fla)

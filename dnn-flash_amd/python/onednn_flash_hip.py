@@ -75,6 +75,7 @@ class AttentionParams(ctypes.Structure):
         ("bias_strides", ctypes.c_int64 * 3),
         ("softcap", ctypes.c_float),
         ("algorithm", ctypes.c_int32),
+        ("max_key_splits", ctypes.c_int32),
     ]
 
 
@@ -88,6 +89,7 @@ class LaunchInfo(ctypes.Structure):
         ("uses_tile_list", ctypes.c_int32),
         ("key_splits", ctypes.c_int32),
         ("kernel_name", ctypes.c_char * 96),
+        ("merge_in_launch", ctypes.c_int32),
     ]
 
 
@@ -180,7 +182,7 @@ def make_params(batch, heads, query_tokens, key_tokens, head_dim, value_dim=None
                 mask_query_block_size=0, mask_key_block_size=0, mask_query_blocks=0,
                 mask_key_blocks=0, bias_kind=BIAS_NONE, alibi_slopes=None, bias=None,
                 bias_strides=(0, 0, 0), softcap=0.0, algorithm=ALGO_AUTO,
-                strides=None) -> AttentionParams:
+                strides=None, max_key_splits=0) -> AttentionParams:
     """Builds an ofh_attention_params. Pointer arguments are integers (device or
     host addresses, as the entry point expects)."""
     p = AttentionParams()
@@ -213,6 +215,7 @@ def make_params(batch, heads, query_tokens, key_tokens, head_dim, value_dim=None
                 arr[i] = s[i]
     p.softcap = softcap
     p.algorithm = algorithm
+    p.max_key_splits = max_key_splits
     return p
 
 
@@ -327,7 +330,7 @@ def _check_attention_inputs(q, k, v, mask, mask_block_size, alibi_slopes, bias, 
 def attention_fwd(q, k, v, *, scale: float | None = None, causal: bool = False, mask=None,
                   mask_block_size: tuple[int, int] = (1, 1), alibi_slopes=None, bias=None,
                   softcap: float = 0.0, out=None, out_dtype=None, algorithm: int = ALGO_AUTO,
-                  workspace=None, stream=None):
+                  workspace=None, stream=None, max_key_splits: int = 0):
     """q: [B,H,M,D], k: [B,H,N,D], v: [B,H,N,Dv] device tensors (f32/bf16/f16, last
     axis contiguous). mask: uint8 device tensor [qblocks, kblocks]. alibi_slopes:
     f32 device [H]. bias: f32 device [M,N] (shared) or [B,H,M,N]. Returns out.
@@ -357,7 +360,8 @@ def attention_fwd(q, k, v, *, scale: float | None = None, causal: bool = False, 
     p = make_params(B, H, M, N, D, Dv, dtype=dtype_code(q.dtype), out_dtype=dtype_code(out.dtype),
                     scale=(1.0 / math.sqrt(D)) if scale is None else scale, causal=causal,
                     bias_kind=bias_kind, softcap=softcap, algorithm=algorithm,
-                    strides=[(t.stride(0), t.stride(1), t.stride(2)) for t in (q, k, v, out)], **kw)
+                    strides=[(t.stride(0), t.stride(1), t.stride(2)) for t in (q, k, v, out)],
+                    max_key_splits=max_key_splits, **kw)
     if stream is None:
         stream = torch.cuda.current_stream(q.device).cuda_stream
     ws_ptr, ws_bytes = (0, 0) if workspace is None else (workspace.data_ptr(), workspace.numel() * workspace.element_size())

@@ -105,6 +105,13 @@ typedef struct ofh_attention_params {
     float softcap;               /* <= 0: disabled */
 
     int32_t algorithm;           /* ofh_algorithm */
+
+    /* Key split of the MFMA kernels (no counterpart in the reference, whose
+     * CPU loop has no workgroups to fill): a call whose query tiles give fewer
+     * workgroups than the GPU holds runs each query tile's keys as several
+     * workgroups and merges their partial rows. 0: the library chooses
+     * (ofh_launch_info.key_splits); 1: never split; n > 1: at most n splits. */
+    int32_t max_key_splits;
 } ofh_attention_params;
 
 /* Fills defaults: struct_size, dtype f32, out_dtype f32, scale 1.0, everything
@@ -113,7 +120,7 @@ void ofh_attention_params_init(ofh_attention_params* p);
 
 /* Bytes of device scratch the forward call needs for these parameters: the
  * per-query-tile list of allowed key tiles when a block mask is given, and the
- * partial rows (unnormalised O, running max and sum) when an fp32 call with few
+ * partial rows (unnormalised O, running max and sum) when a call with few
  * query tiles splits each query tile's keys over several workgroups (see
  * ofh_launch_info.key_splits); 0 otherwise. */
 int ofh_attention_workspace_bytes(const ofh_attention_params* p, size_t* bytes);
@@ -125,6 +132,15 @@ int ofh_attention_workspace_bytes(const ofh_attention_params* p, size_t* bytes);
  * buffer and calls hipMalloc. Such a call blocks the host, so callers that
  * must not block or allocate (HIP graph capture, framework ops with their own
  * allocator) pass a workspace of ofh_attention_workspace_bytes bytes instead.
+ * On a stream under graph capture with workspace NULL, a key split that does
+ * not fit the stream's buffer is dropped (same result, one workgroup per
+ * query tile); block-mask tile lists still need a workspace there.
+ * A key split with few rows per query tile (ofh_launch_info.merge_in_launch)
+ * merges its partial rows in the launch itself, counting arrivals in a
+ * counter slot that the library keeps per (device, stream) for up to 63
+ * streams (later streams merge in a second launch); a captured graph keeps
+ * its stream's slot, so replays of one graph must not overlap each other or
+ * calls on that stream.
  * Calls from several host threads are safe: a thread holds the library's lock
  * from choosing the buffer until its launches are queued, and calls on
  * different streams never share a buffer.
@@ -167,8 +183,12 @@ typedef struct ofh_launch_info {
     int64_t workgroups;       /* grid size of the attention kernel */
     int32_t uses_tile_list;   /* 1 when a block-mask tile list is built first */
     int32_t key_splits;       /* workgroups per query tile, each over a range of K/V
-                                 tiles; > 1 adds a kernel that merges the partial rows */
+                                 tiles, whose partial rows are then merged */
     char kernel_name[96];
+    int32_t merge_in_launch;  /* key_splits > 1: 1 when the split workgroup that finishes
+                                 last merges its query tile (few rows per tile; needs a free
+                                 counter slot, see ofh_attention_fwd), 0 when a second
+                                 kernel merges the partial rows */
 } ofh_launch_info;
 
 int ofh_attention_launch_info(const ofh_attention_params* p, ofh_launch_info* info);

@@ -151,6 +151,8 @@ def test_validation_messages(ofh):
                   F.OFH_ERROR_INVALID_ARGUMENT, "slopes")
     _expect_error(F, F.make_params(1, 1, 4, 4, 96, algorithm=F.ALGO_FLASH_MFMA),
                   F.OFH_ERROR_UNSUPPORTED, "flash MFMA kernel needs")
+    _expect_error(F, F.make_params(1, 1, 4, 4, 64, max_key_splits=-1), F.OFH_ERROR_INVALID_ARGUMENT,
+                  "max_key_splits")
     p = F.make_params(1, 1, 4, 4, 64)
     p.struct_size = 8
     _expect_error(F, p, F.OFH_ERROR_INVALID_ARGUMENT, "struct_size")
@@ -187,6 +189,18 @@ def test_kernel_choice(ofh):
     info = F.launch_info(F.make_params(4, 32, 4096, 4096, 128, dtype=F.DTYPE_BF16, causal=True))
     # causal: query tiles nqt-1-p and p share a workgroup
     assert info.workgroups == 4 * 32 * 8 and info.block_m == 256 and info.threads == 512
+    assert info.key_splits == 1
+    # 16-bit decode: 8 heads x 1 query tile -> 256 staged 128-key tiles per head
+    # in 64 splits of 4 (512 workgroups)
+    info = F.launch_info(F.make_params(1, 8, 1, 32768, 128, dtype=F.DTYPE_BF16))
+    assert info.key_splits == 64 and info.workgroups == 8 * 64
+    assert F.launch_info(F.make_params(1, 8, 1, 32768, 128, dtype=F.DTYPE_BF16,
+                                       max_key_splits=1)).key_splits == 1
+    assert F.launch_info(F.make_params(1, 8, 1, 32768, 128, dtype=F.DTYPE_BF16,
+                                       max_key_splits=3)).key_splits == 3
+    # causal with too few pairs: unpaired query tiles (16 per head), split
+    info = F.launch_info(F.make_params(1, 8, 4096, 4096, 128, dtype=F.DTYPE_BF16, causal=True))
+    assert info.key_splits == 7 and info.workgroups == 8 * 16 * 7
     info = F.launch_info(F.make_params(4, 32, 4096, 4096, 128, dtype=F.DTYPE_BF16))
     assert info.workgroups == 4 * 32 * 16
     assert info.key_splits == 1 and info.block_n == 128   # staged keys per barrier (2 x 64 computed)
@@ -233,13 +247,23 @@ def test_useful_flops_match_workloads(ofh):
 
 def test_workspace_bytes(ofh):
     F = ofh
-    assert F.workspace_bytes(F.make_params(1, 1, 512, 512, 64, dtype=F.DTYPE_BF16)) == 0
+    assert F.workspace_bytes(F.make_params(1, 1, 512, 512, 64, dtype=F.DTYPE_BF16, max_key_splits=1)) == 0
+    # key split: [partial O (fp32)] then [(m, l) per row], per split
+    p = F.make_params(1, 1, 512, 512, 64, dtype=F.DTYPE_BF16)
+    splits = F.launch_info(p).key_splits
+    assert splits == 4  # 4 staged 128-key tiles, one per split
+    assert F.workspace_bytes(p) == splits * 512 * 64 * 4 + splits * 512 * 8
     m = np.ones((8, 8), np.uint8)
-    p = F.make_params(1, 1, 512, 512, 64, dtype=F.DTYPE_BF16, mask_allowed=m.ctypes.data,
-                      mask_query_block_size=64, mask_key_block_size=64, mask_query_blocks=8,
-                      mask_key_blocks=8)
+    mk = dict(mask_allowed=m.ctypes.data, mask_query_block_size=64, mask_key_block_size=64,
+              mask_query_blocks=8, mask_key_blocks=8)
+    p = F.make_params(1, 1, 512, 512, 64, dtype=F.DTYPE_BF16, max_key_splits=1, **mk)
     nqt, nkt = 4, 8  # 128-row query tiles (block-mask schedule), 64-key tiles
     assert F.workspace_bytes(p) == 256 + nqt * nkt * 4
+    p = F.make_params(1, 1, 512, 512, 64, dtype=F.DTYPE_BF16, **mk)
+    splits = F.launch_info(p).key_splits
+    assert splits == 8
+    lists = -(-(256 + nqt * nkt * 4) // 256) * 256  # tile lists, then 256-byte aligned partial rows
+    assert F.workspace_bytes(p) == lists + splits * 512 * 64 * 4 + splits * 512 * 8
 
 
 def test_attention_fwd_rejects_mismatched_inputs_before_launch(ofh):

@@ -77,12 +77,15 @@ SHAPES = [(1, 1), (7, 13), (64, 64), (128, 128), (200, 333), (333, 200), (1, 204
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("causal", [False, True])
-def test_mfma_shapes(ofh, dt, D, causal):
+@pytest.mark.parametrize("splits", [1, 0])
+def test_mfma_shapes(ofh, dt, D, causal, splits):
+    """splits=1: one workgroup per query tile (causal 16-bit: paired tiles);
+    splits=0: the library's key split, which these few-tile shapes take."""
     for i, (M, N) in enumerate(SHAPES):
         dev, host = make_inputs(dt, 2, 3, M, N, D, seed=i)
-        out = run(ofh, dev, dt=dt, causal=causal)
+        out = run(ofh, dev, dt=dt, causal=causal, max_key_splits=splits)
         ref = oracle_full(host, causal=causal)
-        check(out, ref, dt, f"{dt} D{D} causal={causal} M{M} N{N}")
+        check(out, ref, dt, f"{dt} D{D} causal={causal} M{M} N{N} max_key_splits={splits}")
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
@@ -232,8 +235,8 @@ KEY_SPLIT_CASES = {
 def test_key_split_fp32(ofh, name):
     """fp32 calls with few query tiles run each query tile's keys as several
     workgroups and merge the partial rows (running max, row sum, unnormalised
-    O) in a second kernel; the merged rows meet the fp32 bar, fully masked rows
-    stay 0, and the workspace query covers the partial rows."""
+    O) in the workgroup that finishes last; the merged rows meet the fp32 bar,
+    fully masked rows stay 0, and the workspace query covers the partial rows."""
     F = ofh
     B, H, M, N, D, causal, ex = KEY_SPLIT_CASES[name]
     p = F.make_params(B, H, M, N, D, dtype=F.DTYPE_F32, causal=causal)
@@ -496,21 +499,25 @@ def rescale_inputs(dt, B, H, M, N, D, seed, sign=1.0, d1=8.5):
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("sign", [1.0, -1.0])
-def test_rescale_with_live_accumulator(ofh, dt, D, sign):
+@pytest.mark.parametrize("splits", [1, 0])
+def test_rescale_with_live_accumulator(ofh, dt, D, sign, splits):
     """Plain-scale kernels (bf16/fp16: the D=64 128-key tile, the D=128 tile
-    staged as two 64-key steps; fp32), causal (paired query tiles) and not,
-    and a negative scale (the min-based raw max of the unmasked tiles)."""
+    staged as two 64-key steps; fp32), causal (paired query tiles when not
+    split) and not, a negative scale (the min-based raw max of the unmasked
+    tiles), each with one workgroup per query tile and with the key split
+    (whose splits each rescale their own partial rows)."""
     N = 2048
     for causal, M in ((False, 300), (True, N)):
         dev, host, scale = rescale_inputs(dt, 1, 2, M, N, D, seed=D + int(sign > 0), sign=sign)
-        out = run(ofh, dev, dt=dt, causal=causal, scale=scale)
+        out = run(ofh, dev, dt=dt, causal=causal, scale=scale, max_key_splits=splits)
         ref = oracle_full(host, causal=causal, scale=scale)
-        check(out, ref, dt, f"{dt} D{D} rescale causal={causal} scale={scale:+.4f}")
+        check(out, ref, dt, f"{dt} D{D} rescale causal={causal} scale={scale:+.4f} max_key_splits={splits}")
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("sign", [1.0, -1.0])
-def test_rescale_with_live_accumulator_block_mask(ofh, dt, sign):
+@pytest.mark.parametrize("splits", [1, 0])
+def test_rescale_with_live_accumulator_block_mask(ofh, dt, sign, splits):
     """The same for the block-mask list kernels (64-key tiles, per-wavefront
     skip bits): a dense 64x64 bitmap with a few blocks of region C removed."""
     N, D = 2048, 64
@@ -521,18 +528,21 @@ def test_rescale_with_live_accumulator_block_mask(ofh, dt, sign):
     for causal, M in ((False, 300), (True, N)):
         dev, host, scale = rescale_inputs(dt, 1, 2, M, N, D, seed=7, sign=sign)
         mq = -(-M // 64)
-        out = run(ofh, dev, dt=dt, causal=causal, scale=scale, mask=mask[:mq], mbs=(64, 64))
+        out = run(ofh, dev, dt=dt, causal=causal, scale=scale, mask=mask[:mq], mbs=(64, 64),
+                  max_key_splits=splits)
         ref = oracle_full(host, causal=causal, scale=scale, mask=mask[:mq], mbs=(64, 64))
-        check(out, ref, dt, f"{dt} list rescale causal={causal} scale={scale:+.4f}")
+        check(out, ref, dt, f"{dt} list rescale causal={causal} scale={scale:+.4f} max_key_splits={splits}")
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
-def test_rescale_with_score_mod(ofh, dt):
+@pytest.mark.parametrize("splits", [1, 0])
+def test_rescale_with_score_mod(ofh, dt, splits):
     """The score_mod kernel (ALiBi + soft-cap) on the same inputs."""
     N, D, H = 2048, 128, 2
     slopes = np.array([1e-3, 2e-3], np.float32)
     for causal, M in ((False, 300), (True, N)):
         dev, host, scale = rescale_inputs(dt, 1, H, M, N, D, seed=9)
-        out = run(ofh, dev, dt=dt, causal=causal, scale=scale, slopes=slopes, softcap=50.0)
+        out = run(ofh, dev, dt=dt, causal=causal, scale=scale, slopes=slopes, softcap=50.0,
+                  max_key_splits=splits)
         ref = oracle_full(host, causal=causal, scale=scale, slopes=slopes, softcap=50.0)
-        check(out, ref, dt, f"{dt} score_mod rescale causal={causal}")
+        check(out, ref, dt, f"{dt} score_mod rescale causal={causal} max_key_splits={splits}")

@@ -1,8 +1,9 @@
 """The allocation-free entry point ofh_attention_fwd_noalloc (no counterpart in
 the reference; for callers that cannot allocate inside the call): through the
 C ABI, against ofh_attention_fwd on the same inputs, for the calls that use
-scratch (block-mask tile lists, fp32 key-split partial rows), twice in a row
-with the second call smaller, plus its size limit."""
+scratch (block-mask tile lists, bf16 and fp32 key-split partial rows, whose
+merge counts arrivals in the entry's own counter slot), twice in a row with
+the second call smaller, plus its size limit."""
 
 from __future__ import annotations
 
@@ -46,15 +47,17 @@ def test_noalloc_matches_fwd(ofh):
         pytest.skip("no GPU")
     F = ofh
     lib = F.lib()
-    cases = [  # (label, dtype, B, H, M, N, D, causal, block mask?)
-        ("bf16 block mask", "bf16", 1, 4, 4096, 4096, 64, True, True),
-        ("bf16 block mask, smaller", "bf16", 1, 2, 1024, 1024, 64, True, True),
-        ("fp32 key split", "f32", 1, 4, 512, 1024, 64, False, False),
-        ("fp32 key split, smaller", "f32", 1, 2, 128, 640, 128, True, False),
+    cases = [  # (label, dtype, B, H, M, N, D, causal, block mask?, max_key_splits)
+        ("bf16 block mask", "bf16", 1, 4, 4096, 4096, 64, True, True, 1),
+        ("bf16 block mask, smaller", "bf16", 1, 2, 1024, 1024, 64, True, True, 1),
+        ("bf16 key split", "bf16", 1, 2, 64, 16384, 128, False, False, 0),
+        ("bf16 key split, smaller", "bf16", 1, 1, 1, 4000, 128, False, False, 0),  # merged in the launch
+        ("fp32 key split", "f32", 1, 4, 256, 1024, 64, False, False, 0),
+        ("fp32 key split, smaller", "f32", 1, 2, 128, 640, 128, True, False, 0),
     ]
     stream = torch.cuda.Stream()
     free_after_first = None
-    for i, (label, dt, B, H, M, N, D, causal, masked) in enumerate(cases):
+    for i, (label, dt, B, H, M, N, D, causal, masked, splits) in enumerate(cases):
         dev, host = make_inputs(dt, B, H, M, N, D, seed=60 + i)
         q, k, v = dev
         kw = {}
@@ -67,7 +70,8 @@ def test_noalloc_matches_fwd(ofh):
                       mask_key_blocks=mask.shape[1])
         code = {"f32": F.DTYPE_F32, "bf16": F.DTYPE_BF16}[dt]
         p = F.make_params(B, H, M, N, D, dtype=code, out_dtype=F.DTYPE_F32, scale=1.0 / math.sqrt(D),
-                          causal=causal, **kw)
+                          causal=causal, max_key_splits=splits, **kw)
+        assert (F.launch_info(p).key_splits > 1) == ("key split" in label), label
         need = F.workspace_bytes(p)
         assert 0 < need <= NOALLOC_MAX, (label, need)
         o_ref = torch.empty((B, H, M, D), device="cuda", dtype=torch.float32)
