@@ -10,7 +10,7 @@ peak, and the algorithmic HBM rate (Q, K, V read once, O written once) against
 8 TB/s, with the kernel choice of ofh_attention_launch_info.
 
     python dnn-flash_amd/bench/bench_shapes.py --shape 1,8,1,32768,128 --dtype bf16 \
-        [--causal] [--max-key-splits S] [--steps K] [--warmup W]
+        [--causal] [--max-key-splits S] [--algorithm auto|mfma|rowwise] [--steps K] [--warmup W]
 """
 
 from __future__ import annotations
@@ -34,6 +34,7 @@ def main() -> int:
     ap.add_argument("--out-dtype", default="f32", choices=["bf16", "f16", "f32"])
     ap.add_argument("--causal", action="store_true")
     ap.add_argument("--max-key-splits", type=int, default=0)
+    ap.add_argument("--algorithm", default="auto", choices=["auto", "mfma", "rowwise"])
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=30)
     args = ap.parse_args()
@@ -50,8 +51,9 @@ def main() -> int:
         k = torch.randn((B, H, N, D), device="cuda", generator=g).to(tdt[args.dtype])
         v = torch.randn((B, H, N, D), device="cuda", generator=g).to(tdt[args.dtype])
         out = torch.empty((B, H, M, D), device="cuda", dtype=tdt[args.out_dtype])
+        algo = {"auto": F.ALGO_AUTO, "mfma": F.ALGO_FLASH_MFMA, "rowwise": F.ALGO_ROWWISE}[args.algorithm]
         p = F.make_params(B, H, M, N, D, dtype=code[args.dtype], out_dtype=code[args.out_dtype],
-                          causal=args.causal, max_key_splits=args.max_key_splits)
+                          causal=args.causal, max_key_splits=args.max_key_splits, algorithm=algo)
         info = F.launch_info(p)
         flops = F.useful_flops(p)
         ws_bytes = F.workspace_bytes(p)
@@ -60,7 +62,7 @@ def main() -> int:
 
         def call():
             F.attention_fwd(q, k, v, scale=scale, causal=args.causal, out=out, workspace=ws,
-                            max_key_splits=args.max_key_splits)
+                            max_key_splits=args.max_key_splits, algorithm=algo)
 
         for _ in range(args.warmup):
             call()

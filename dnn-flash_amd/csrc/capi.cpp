@@ -192,8 +192,8 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
             if (((s[i] * (int64_t)esz) & 15) != 0) return false;
         return true;
     };
-    const bool mfma_ok = p->head_dim == p->value_dim &&
-                         (p->head_dim == 64 || p->head_dim == 128) &&
+    const bool mfma_ok = p->head_dim == p->value_dim && p->head_dim <= 256 &&
+                         ofh::flash_mfma_head_dim(p->dtype, (int)p->head_dim) &&
                          (p->dtype != OFH_DTYPE_F32 || p->out_dtype == OFH_DTYPE_F32) &&
                          aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) &&
                          strides_ok(r.qs, es) && strides_ok(r.ks, es) && strides_ok(r.vs, es) &&
@@ -202,7 +202,8 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
                          std::llabs((long long)r.ks[2]) <= (1 << 24) && std::llabs((long long)r.vs[2]) <= (1 << 24);
     if (p->algorithm == OFH_ALGO_FLASH_MFMA && !mfma_ok)
         return set_error(OFH_ERROR_UNSUPPORTED,
-                         "flash MFMA kernel needs head_dim == value_dim in {64, 128}, 16-byte "
+                         "flash MFMA kernel needs head_dim == value_dim in {32, 64, 128} (and 256 for "
+                         "bf16/fp16), 16-byte "
                          "aligned rows and K/V token strides of at most 2^24 elements; use "
                          "OFH_ALGO_AUTO or OFH_ALGO_ROWWISE");
     if (p->algorithm == OFH_ALGO_ROWWISE || !mfma_ok) {

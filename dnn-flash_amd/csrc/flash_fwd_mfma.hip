@@ -30,6 +30,8 @@
 
 #include <map>
 #include <mutex>
+#include <string>
+#include <vector>
 
 #include "ofh_kernels.h"
 
@@ -459,8 +461,24 @@ template <int D, int BN>
 struct TileLayout {
     static constexpr int RB = D * 2;              // bytes of one K/V row
     static constexpr int CPR = D / 8;             // 16-byte chunks per row
-    static __device__ __forceinline__ int kswz(int row) { return D == 128 ? (row & 15) : ((row >> 1) & 7); }
-    static __device__ __forceinline__ int vswz(int row) { return D == 128 ? 4 * (row & 3) : 4 * ((row >> 1) & 1); }
+    static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head dims of the 16-bit kernels");
+    // Both swizzles must repeat every 8 rows or less at D = 256 (every 16 at
+    // D = 128, 32 at D = 64, 64 at D = 32): a copy lane reuses one swizzled
+    // chunk offset for the rows DSTEP = 64 * wavefronts / CPR apart that it
+    // copies (8 rows with 4 wavefronts at D = 256). The V swizzle must also
+    // repeat every 4 rows: a V^T fragment is two transposing reads 4 rows
+    // apart at one lane offset.
+    static __device__ __forceinline__ int kswz(int row) {
+        if (D == 256) return row & 7;
+        if (D == 128) return row & 15;
+        if (D == 64) return (row >> 1) & 7;
+        return (row >> 2) & 3;  // D = 32: four rows share a bank line
+    }
+    static __device__ __forceinline__ int vswz(int row) {
+        if (D >= 128) return 4 * (row & 3);
+        if (D == 64) return 4 * ((row >> 1) & 1);
+        return 0;  // D = 32: a row is one 32-column block
+    }
     static constexpr int KSTR = RB;
     static constexpr int VSTR = RB;
     static constexpr int KTILE = BN * KSTR;
@@ -532,6 +550,8 @@ struct Wave32 {
     int k_lane_off, v_lane_off;
     // K/V copies: lane offsets (elements) of its chunk in rows dma_row0 + u*DSTEP
     static constexpr int DSTEP = 64 * (NTHREADS / 64) / L::CPR;
+    static_assert(DSTEP % (D == 256 ? 8 : D == 128 ? 16 : D == 64 ? 32 : 64) == 0,
+                  "the K/V swizzles must repeat within the rows one copy lane covers");
     int dma_row0, dma_koff, dma_voff;
 
     __device__ __forceinline__ Wave32(const FwdArgs& args, unsigned char* sm, int bh, int q0, int wv)
@@ -1064,8 +1084,10 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
     finish_qtile<W, NTHREADS, SPLIT>(a, w, smem, bh, qt, q0, BLOCK_M, split, active);
 }
 
+// D = 256 runs one 4-wavefront workgroup per CU (one wavefront per SIMD, so
+// the O accumulators can use the accumulation registers).
 template <typename T, int D, int MOD, bool LIST, int NWAVES, bool PAIRED, int BN = kBlockN16, int SB = 1>
-__global__ __launch_bounds__(NWAVES * 64, 8 / NWAVES) void flash_fwd_lockstep_kernel(FwdArgs a) {
+__global__ __launch_bounds__(NWAVES * 64, (D == 256 ? 4 : 8) / NWAVES) void flash_fwd_lockstep_kernel(FwdArgs a) {
     using L = TileLayout<D, BN * SB>;
     __shared__ __attribute__((aligned(16))) unsigned char smem[2 * L::STAGE];
     int bh, qts[2];
@@ -1365,14 +1387,12 @@ hipError_t launch(K kernel, int threads, const FwdArgs& a, hipStream_t s, bool p
 
 }  // namespace
 
-// 16-bit kernel schedule for a call: 8 wavefronts (256 query rows) without a
-// block-mask list, 4 wavefronts (128 rows, finer skipping) with one.
-enum Sched16 { SCHED_LOCKSTEP8 = 0, SCHED_LOCKSTEP4 = 1 };
+// 16-bit kernel workgroups: 8 wavefronts (256 query rows) without a
+// block-mask list, 4 wavefronts (128 rows, finer skipping) with one, and 4
+// wavefronts at D = 256 (register file).
 
 // Causal calls without a block-mask list pair query tiles per workgroup.
 static bool pairs_causal_tiles(bool causal, bool tile_list) { return causal && !tile_list; }
-
-static int sched16(bool tile_list) { return tile_list ? SCHED_LOCKSTEP4 : SCHED_LOCKSTEP8; }
 
 // Keys per staged K/V tile (one barrier each) of a 16-bit call: 128 without
 // score_mod or block mask (half the barriers and tile stores per key), else 64
@@ -1380,8 +1400,13 @@ static int sched16(bool tile_list) { return tile_list ? SCHED_LOCKSTEP4 : SCHED_
 // kernel holds all fragments of a tile). At D = 64 the 128 keys are one compute
 // step (+9 to +13 %); at D = 128, where S and P for 128 keys would spill, they
 // are computed in two 64-key steps between the same barriers (+1 to +5 %).
-static int block_n16(bool general_mod, bool tile_list) {
-    return (!general_mod && !tile_list) ? kBlockN16Wide : kBlockN16;
+// D = 32 stages 128 keys in every kernel without a block mask (a 64-key tile
+// of 64-byte rows is fewer 16-byte chunks than the 8 wavefronts copy), and
+// D = 256 runs 4 wavefronts (128 query rows) on 64-key tiles throughout.
+static int block_n16(int D, bool general_mod, bool tile_list) {
+    if (D == 256 || tile_list) return kBlockN16;
+    if (D == 32) return kBlockN16Wide;
+    return !general_mod ? kBlockN16Wide : kBlockN16;
 }
 
 template <typename T, int D>
@@ -1391,24 +1416,41 @@ static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
     if (list)
         return general_mod ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, true, 4, false>, 256, a, s)
                            : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, true, 4, false>, 256, a, s);
-    if (general_mod)
-        return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8, true>, 512, a, s, true)
-                      : launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8, false>, 512, a, s);
-    // D = 64: 128-key tiles; D = 128: 128 keys staged per barrier, two 64-key compute steps (block_n16)
-    constexpr int BN = D == 64 ? kBlockN16Wide : kBlockN16;
-    constexpr int SB = D == 64 ? 1 : kBlockN16Wide / kBlockN16;
-    return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, true, BN, SB>, 512, a, s, true)
-                  : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, false, BN, SB>, 512, a, s);
+    if constexpr (D == 256) {
+        if (general_mod)
+            return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 4, true>, 256, a, s, true)
+                          : launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 4, false>, 256, a, s);
+        return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 4, true>, 256, a, s, true)
+                      : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 4, false>, 256, a, s);
+    } else {
+        // score_mod: 64-key compute steps (two per staged tile at D = 32)
+        constexpr int GSB = D == 32 ? 2 : 1;
+        if (general_mod)
+            return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8, true, kBlockN16, GSB>, 512, a, s, true)
+                          : launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8, false, kBlockN16, GSB>, 512, a, s);
+        // D <= 64: 128-key tiles; D = 128: 128 keys staged per barrier, two 64-key compute steps
+        constexpr int BN = D <= 64 ? kBlockN16Wide : kBlockN16;
+        constexpr int SB = D <= 64 ? 1 : kBlockN16Wide / kBlockN16;
+        return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, true, BN, SB>, 512, a, s, true)
+                      : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, false, BN, SB>, 512, a, s);
+    }
 }
 
 hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipStream_t s) {
     if (dtype == DT_BF16) {
+        if (a.D == 32) return launch16<__bf16, 32>(a, general_mod, s);
         if (a.D == 64) return launch16<__bf16, 64>(a, general_mod, s);
         if (a.D == 128) return launch16<__bf16, 128>(a, general_mod, s);
+        if (a.D == 256) return launch16<__bf16, 256>(a, general_mod, s);
     } else if (dtype == DT_F16) {
+        if (a.D == 32) return launch16<_Float16, 32>(a, general_mod, s);
         if (a.D == 64) return launch16<_Float16, 64>(a, general_mod, s);
         if (a.D == 128) return launch16<_Float16, 128>(a, general_mod, s);
+        if (a.D == 256) return launch16<_Float16, 256>(a, general_mod, s);
     } else if (dtype == DT_F32) {
+        if (a.D == 32)
+            return general_mod ? launch(flash_fwd_mfma32_kernel<32, true, kTilesF32>, kThreads32, a, s)
+                               : launch(flash_fwd_mfma32_kernel<32, false, kTilesF32>, kThreads32, a, s);
         if (a.D == 64)
             return general_mod ? launch(flash_fwd_mfma32_kernel<64, true, kTilesF32>, kThreads32, a, s)
                                : launch(flash_fwd_mfma32_kernel<64, false, kTilesF32>, kThreads32, a, s);
@@ -1463,31 +1505,47 @@ hipError_t split_counter_slot(int slot, unsigned** ptr) {
     return hipSuccess;
 }
 
+bool flash_mfma_head_dim(int dtype, int D) {
+    if (dtype == DT_F32) return D == 32 || D == 64 || D == 128;
+    return D == 32 || D == 64 || D == 128 || D == 256;
+}
+
 const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile_list) {
-    if (dtype < 0 || dtype > 2 || (D != 64 && D != 128)) return "none";
-    static const char* f32names[2][2] = {
-        {"flash_fwd_mfma32_kernel<64,plain>", "flash_fwd_mfma32_kernel<64,general>"},
-        {"flash_fwd_mfma32_kernel<128,plain>", "flash_fwd_mfma32_kernel<128,general>"}};
-    if (dtype == DT_F32) return f32names[D == 128][general_mod ? 1 : 0];
-    // [f16][D==128][score_mod][list]
-    static const char* names[2][2][2][2] = {
-        {{{"flash_fwd_lockstep_kernel<bf16,64,plain,8w,128keys>", "flash_fwd_lockstep_kernel<bf16,64,plain,list,4w>"},
-          {"flash_fwd_lockstep_kernel<bf16,64,mod,8w>", "flash_fwd_lockstep_kernel<bf16,64,mod,list,4w>"}},
-         {{"flash_fwd_lockstep_kernel<bf16,128,plain,8w,2x64keys>", "flash_fwd_lockstep_kernel<bf16,128,plain,list,4w>"},
-          {"flash_fwd_lockstep_kernel<bf16,128,mod,8w>", "flash_fwd_lockstep_kernel<bf16,128,mod,list,4w>"}}},
-        {{{"flash_fwd_lockstep_kernel<f16,64,plain,8w,128keys>", "flash_fwd_lockstep_kernel<f16,64,plain,list,4w>"},
-          {"flash_fwd_lockstep_kernel<f16,64,mod,8w>", "flash_fwd_lockstep_kernel<f16,64,mod,list,4w>"}},
-         {{"flash_fwd_lockstep_kernel<f16,128,plain,8w,2x64keys>", "flash_fwd_lockstep_kernel<f16,128,plain,list,4w>"},
-          {"flash_fwd_lockstep_kernel<f16,128,mod,8w>", "flash_fwd_lockstep_kernel<f16,128,mod,list,4w>"}}}};
-    return names[dtype == DT_F16][D == 128][general_mod ? 1 : 0][tile_list ? 1 : 0];
+    if (dtype < 0 || dtype > 2 || !flash_mfma_head_dim(dtype, D)) return "none";
+    // [dtype][log2(D) - 5][score_mod][list]
+    static const std::vector<std::string> names = [] {
+        std::vector<std::string> v;
+        const char* tn[3] = {"f32", "bf16", "f16"};
+        for (int dt = 0; dt < 3; ++dt)
+            for (int d = 32; d <= 256; d *= 2)
+                for (int mod = 0; mod < 2; ++mod)
+                    for (int list = 0; list < 2; ++list) {
+                        std::string n;
+                        if (dt == DT_F32) {
+                            n = "flash_fwd_mfma32_kernel<" + std::to_string(d) + (mod ? ",general>" : ",plain>");
+                        } else {
+                            n = std::string("flash_fwd_lockstep_kernel<") + tn[dt] + "," + std::to_string(d) +
+                                (mod ? ",mod" : ",plain");
+                            if (list) n += ",list,4w>";
+                            else if (d == 256) n += ",4w>";
+                            else if (!mod && d <= 64) n += ",8w,128keys>";
+                            else if (!mod && d == 128) n += ",8w,2x64keys>";
+                            else if (mod && d == 32) n += ",8w,2x64keys>";
+                            else n += ",8w>";
+                        }
+                        v.push_back(n);
+                    }
+        return v;
+    }();
+    const int di = D == 32 ? 0 : D == 64 ? 1 : D == 128 ? 2 : 3;
+    return names[(((size_t)dtype * 4 + di) * 2 + (general_mod ? 1 : 0)) * 2 + (tile_list ? 1 : 0)].c_str();
 }
 
 MfmaTiles flash_mfma_tiles(int dtype, int D, bool general_mod, bool tile_list, bool causal) {
     if (dtype == DT_F32) return MfmaTiles{kBlockM32, kBlockNF32 * kTilesF32, kThreads32, false};
     const bool paired = pairs_causal_tiles(causal, tile_list);
-    (void)D;
-    const int bn = block_n16(general_mod, tile_list);
-    if (sched16(tile_list) == SCHED_LOCKSTEP4) return MfmaTiles{128, bn, 256, paired};
+    const int bn = block_n16(D, general_mod, tile_list);
+    if (tile_list || D == 256) return MfmaTiles{128, bn, 256, paired};
     return MfmaTiles{256, bn, 512, paired};
 }
 

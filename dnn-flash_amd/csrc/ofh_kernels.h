@@ -131,6 +131,8 @@ hipError_t launch_qk_score(const QkScoreArgs& a, int dtype, hipStream_t s);
 bool qk_score_mfma_supported(const QkScoreArgs& a, int dtype);
 hipError_t launch_qk_score_mfma(const QkScoreArgs& a, int dtype, hipStream_t s);
 
+// Head dims (D == Dv) the MFMA kernels are built for: 32, 64, 128 (fp32) and 256 (bf16/fp16).
+bool flash_mfma_head_dim(int dtype, int D);
 const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile_list);
 // Workgroup tiling of the MFMA kernel for a dtype.
 MfmaTiles flash_mfma_tiles(int dtype, int head_dim, bool general_mod, bool tile_list, bool causal);

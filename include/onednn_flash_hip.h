@@ -62,7 +62,7 @@ typedef enum ofh_bias_kind {
 } ofh_bias_kind;
 
 /* Which kernel family runs. AUTO picks the MFMA flash kernel when the shape
- * is supported (D == Dv in {64, 128}, 16-byte aligned rows) and the rowwise
+ * is supported (D == Dv in {32, 64, 128}, or 256 for bf16/fp16; 16-byte aligned rows) and the rowwise
  * kernel otherwise. ROWWISE is the exact two-pass softmax of
  * standard_attention, run on the GPU one query row per wavefront. */
 typedef enum ofh_algorithm {

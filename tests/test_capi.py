@@ -178,6 +178,14 @@ def test_kernel_choice(ofh):
               mask_key_block_size=64, mask_query_blocks=4, mask_key_blocks=4),
          "flash_fwd_lockstep_kernel<f16,64,plain,list,4w>"),
         (dict(dtype=F.DTYPE_BF16, head_dim=96), "rowwise_fwd_kernel"),
+        (dict(dtype=F.DTYPE_BF16, head_dim=32), "flash_fwd_lockstep_kernel<bf16,32,plain,8w,128keys>"),
+        (dict(dtype=F.DTYPE_F16, head_dim=32, softcap=5.0), "flash_fwd_lockstep_kernel<f16,32,mod,8w,2x64keys>"),
+        (dict(dtype=F.DTYPE_BF16, head_dim=256), "flash_fwd_lockstep_kernel<bf16,256,plain,4w>"),
+        (dict(dtype=F.DTYPE_F16, head_dim=256, mask_allowed=16, mask_query_block_size=64,
+              mask_key_block_size=64, mask_query_blocks=5, mask_key_blocks=4),
+         "flash_fwd_lockstep_kernel<f16,256,plain,list,4w>"),
+        (dict(dtype=F.DTYPE_F32, head_dim=32), "flash_fwd_mfma32_kernel<32,plain>"),
+        (dict(dtype=F.DTYPE_F32, head_dim=256), "rowwise_fwd_kernel"),
         (dict(dtype=F.DTYPE_BF16, head_dim=64, value_dim=128), "rowwise_fwd_kernel"),
         (dict(dtype=F.DTYPE_F32, head_dim=64, algorithm=F.ALGO_ROWWISE), "rowwise_fwd_kernel"),
     ]

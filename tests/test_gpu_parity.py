@@ -75,7 +75,7 @@ SHAPES = [(1, 1), (7, 13), (64, 64), (128, 128), (200, 333), (333, 200), (1, 204
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("splits", [1, 0])
 def test_mfma_shapes(ofh, dt, D, causal, splits):
@@ -546,3 +546,38 @@ def test_rescale_with_score_mod(ofh, dt, splits):
                   max_key_splits=splits)
         ref = oracle_full(host, causal=causal, scale=scale, slopes=slopes, softcap=50.0)
         check(out, ref, dt, f"{dt} score_mod rescale causal={causal} max_key_splits={splits}")
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("D", [32, 256])
+def test_head_dims_32_and_256(ofh, dt, D):
+    """The MFMA kernels at D = 32 (bf16/fp16/fp32) and D = 256 (bf16/fp16):
+    ALiBi + soft-cap, a dense bias, a block mask (the list kernel), and the
+    lazy rescale with a live accumulator and a negative scale, each with one
+    workgroup per query tile and with the key split."""
+    F = ofh
+    if dt == "f32" and D == 256:
+        pytest.skip("fp32 runs D = 256 on the rowwise kernel")
+    B, H, M, N = 1, 2, 300, 700
+    code = {"f32": F.DTYPE_F32, "bf16": F.DTYPE_BF16, "f16": F.DTYPE_F16}[dt]
+    assert F.launch_info(F.make_params(B, H, M, N, D, dtype=code)).algorithm == F.ALGO_FLASH_MFMA
+    dev, host = make_inputs(dt, B, H, M, N, D, seed=D)
+    slopes = alibi_slopes(H)
+    bias = O.normal(41, (M, N), std=1.5)
+    rng = np.random.default_rng(D)
+    mask = (rng.random((-(-M // 64), -(-N // 64))) < 0.5).astype(np.uint8)
+    mask[:, 0] = 1
+    for splits in (1, 0):
+        for causal in (False, True):
+            for kw in (dict(slopes=slopes, softcap=30.0), dict(mask=mask, mbs=(64, 64))):
+                out = run(ofh, dev, dt=dt, causal=causal, max_key_splits=splits, **kw)
+                check(out, oracle_full(host, causal=causal, **kw), dt,
+                      f"{dt} D{D} {sorted(kw)} causal={causal} max_key_splits={splits}")
+        out = run(ofh, dev, dt=dt, bias=bias, max_key_splits=splits)
+        check(out, oracle_full(host, bias=bias), dt, f"{dt} D{D} dense bias max_key_splits={splits}")
+        for sign in (1.0, -1.0):
+            rdev, rhost, scale = rescale_inputs(dt, 1, 2, 257, 2048, D, seed=D + 1, sign=sign)
+            for causal in (False, True):
+                out = run(ofh, rdev, dt=dt, causal=causal, scale=scale, max_key_splits=splits)
+                check(out, oracle_full(rhost, causal=causal, scale=scale), dt,
+                      f"{dt} D{D} rescale causal={causal} scale={scale:+.4f} max_key_splits={splits}")
