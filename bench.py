@@ -10,7 +10,11 @@ and a CPU baseline: the reference's own CPU flash path (compiled from its
 sources into oracle/_ref) on a bounded sample of the same workload, run on the
 host cores (the oracle's restatement when oracle/_ref is absent).
 
-    python bench.py [--steps K] [--warmup W] [--workload c3] [--no-cpu-baseline]
+Before the W warm-up steps, untimed steps run for --settle-seconds (default 1 s)
+so that the clocks have left their idle state: with the driver's short warm-up
+the first launches of a cold GPU would otherwise be timed.
+
+    python bench.py [--steps K] [--warmup W] [--workload c3] [--settle-seconds S] [--no-cpu-baseline]
 """
 
 from __future__ import annotations
@@ -37,6 +41,9 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="c3")
+    ap.add_argument("--settle-seconds", type=float, default=1.0,
+                    help="untimed steps for this long before the warm-up, so that the GPU "
+                         "clocks have left their idle state when the warm-up starts (0: none)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="0: the CPU affinity set, capped by OMP_NUM_THREADS when set")
@@ -208,6 +215,17 @@ def main() -> int:
         if rc:
             raise F.OfhError(rc, lib.ofh_last_error().decode())
 
+    # The GPU leaves its idle clocks over the first ~40 launches of the
+    # headline workload; with a short warm-up (5 steps) those slow launches
+    # fall into the timed window. Untimed steps for settle_seconds first, then
+    # the W warm-up steps, then the K timed steps.
+    settle_steps = 0
+    t_settle = time.perf_counter()
+    while time.perf_counter() - t_settle < args.settle_seconds:
+        for _ in range(10):
+            step()
+        settle_steps += 10
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -261,6 +279,7 @@ def main() -> int:
                       "p10": round(pct(0.1), 5), "p90": round(pct(0.9), 5),
                       "min": round(srt[0], 5), "max": round(srt[-1], 5)},
         "wall_s_timed": round(wall, 4),
+        "settle": {"seconds": args.settle_seconds, "steps": settle_steps},
         "roofline": {
             "bound": "mfma",
             "achieved": round(achieved, 3),
