@@ -40,7 +40,8 @@ struct Resolved {
     int64_t qs[3], ks[3], vs[3], os[3];
     int algorithm;       // OFH_ALGO_FLASH_MFMA or OFH_ALGO_ROWWISE
     bool general_mod;    // bias or soft-cap present
-    bool tile_list;      // block-mask tile lists are built
+    bool tile_list;      // block-mask tile lists are used
+    bool lds_list;       // ... built by each workgroup in LDS (no tile_list launch, no workspace)
     int block_m, block_n, threads;
     bool paired;         // causal query tiles run in pairs per workgroup
     int num_q_tiles, num_k_tiles;
@@ -167,6 +168,13 @@ void choose_key_splits(const ofh_attention_params* p, Resolved& r) {
     r.paired = false;
 }
 
+// 16-bit block-mask calls without a key split build each query tile's list
+// in the workgroup's LDS when it fits (at most kLdsListMaxTiles key tiles).
+void set_lds_list(const ofh_attention_params* p, Resolved& r) {
+    r.lds_list = r.tile_list && p->dtype != OFH_DTYPE_F32 && r.key_splits == 1 &&
+                 r.num_k_tiles <= ofh::kLdsListMaxTiles;
+}
+
 void no_key_split(const ofh_attention_params* p, Resolved& r) {
     const ofh::MfmaTiles t =
         ofh::flash_mfma_tiles(p->dtype, (int)p->head_dim, r.general_mod, r.tile_list, p->causal != 0);
@@ -175,6 +183,7 @@ void no_key_split(const ofh_attention_params* p, Resolved& r) {
     r.paired = t.paired;
     r.block_n = t.block_n;
     r.num_k_tiles = (int)((p->key_tokens + r.block_n - 1) / r.block_n);
+    set_lds_list(p, r);
 }
 
 int resolve(const ofh_attention_params* p, const void* q, const void* k, const void* v,
@@ -211,6 +220,7 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
         if (p->head_dim > 1024)
             return set_error(OFH_ERROR_UNSUPPORTED, "rowwise kernel supports head_dim <= 1024");
         r.tile_list = false;
+        r.lds_list = false;
         r.paired = false;
         r.block_m = 1;
         r.block_n = 64;
@@ -240,6 +250,7 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
     if (r.tile_list && (r.block_m > ofh::kQueriesPerWave * ofh::kListSlices || r.num_k_tiles > (1 << 22)))
         return set_error(OFH_ERROR_UNSUPPORTED, "block-mask tile list entry cannot encode this tiling");
     choose_key_splits(p, r);
+    set_lds_list(p, r);
     return OFH_SUCCESS;
 }
 
@@ -248,7 +259,7 @@ size_t round256(size_t n) { return (n + 255) & ~size_t(255); }
 // Workspace layout: [tile counts][tile entries] (block mask), then
 // [partial O][partial (m, l)] (key split).
 size_t list_bytes(const Resolved& r) {
-    if (!r.tile_list) return 0;
+    if (!r.tile_list || r.lds_list) return 0;
     return round256((size_t)r.num_q_tiles * 4) + (size_t)r.num_q_tiles * (size_t)r.num_k_tiles * 4;
 }
 size_t partial_rows(const ofh_attention_params* p, const Resolved& r) {
@@ -422,7 +433,7 @@ int fwd_impl(const ofh_attention_params* p, const void* q, const void* k, const 
                              "workspace too small: need " + std::to_string(need) + " bytes");
         }
     }
-    if (r.tile_list) {
+    if (r.tile_list && !r.lds_list) {
         const size_t counts_bytes = round256((size_t)r.num_q_tiles * 4);
         ofh::TileListArgs t;
         t.M = a.M;
@@ -532,9 +543,14 @@ int ofh_attention_fwd_noalloc(const ofh_attention_params* p, const void* q, cons
                              " bytes of scratch; the allocation-free entry holds at most " +
                              std::to_string(ofh::kNoAllocScratchBytes) +
                              " (use ofh_attention_fwd with a workspace)");
+    // The static arrays (scratch, split counters) are looked up on every call:
+    // the first call on a device materialises them there, whether or not this
+    // call needs them, so no later call changes the device's memory.
     void* ws = nullptr;
-    if (need > 0) OFH_HIP_CHECK(ofh::noalloc_scratch(&ws));
-    return fwd_impl(p, q, k, v, out, ws, need > 0 ? ofh::kNoAllocScratchBytes : 0,
+    OFH_HIP_CHECK(ofh::noalloc_scratch(&ws));
+    unsigned* counters = nullptr;
+    OFH_HIP_CHECK(ofh::split_counter_slot(0, &counters));
+    return fwd_impl(p, q, k, v, out, need > 0 ? ws : nullptr, need > 0 ? ofh::kNoAllocScratchBytes : 0,
                     static_cast<hipStream_t>(stream), true);
 }
 

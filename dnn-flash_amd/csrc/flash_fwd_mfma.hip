@@ -56,6 +56,14 @@ constexpr float kNegInf = -__builtin_huge_valf();
 // prefetch) at each use.
 __device__ __forceinline__ void wait_vm_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// s_waitcnt vmcnt(N): at most N vector-memory operations still outstanding
+// (they complete in issue order, so every older one has completed).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 __device__ __forceinline__ int kappa(int r) {
     return ((r >> 4) << 4) | (((r >> 2) & 1) << 3) | (((r >> 3) & 1) << 2) | (r & 3);
 }
@@ -977,6 +985,121 @@ __device__ __forceinline__ void finish_qtile(const FwdArgs& a, W& w, unsigned ch
         merge_split_rows<typename W::T_, NTHREADS>(a, bh, q0, min(block_m, a.M - q0), active, (float*)smem);
 }
 
+typedef __attribute__((address_space(3))) int lds_int;
+
+// Block-mask list of query tile q0 built by its own workgroup, in LDS: the key
+// tiles (in order) that hold a pair allowed by the mask and the causal rule
+// for some 32-row slice, each with per-slice any/all bits (list_entry), the
+// list the tile_list kernel builds in global memory (rowwise_fwd.hip). One key
+// tile per thread and round; compacted with a per-wavefront ballot and a
+// prefix over the wavefronts' counts. Returns the entry count (uniform).
+template <int NWAVES>
+__device__ int build_tile_list_lds(const FwdArgs& a, int q0, int block_n, lds_int* list, lds_int* wave_counts) {
+    constexpr int NT = NWAVES * 64;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int count = 0;
+    for (int base = 0; base < a.num_k_tiles; base += NT) {
+        const int kt = base + tid;
+        unsigned any_bits = 0, full_bits = 0;
+        if (kt < a.num_k_tiles) {
+            const int k0 = kt * block_n, k1 = min(a.N, k0 + block_n);
+#pragma unroll
+            for (int w = 0; w < NWAVES; ++w) {
+                const int s0 = q0 + kQueriesPerWave * w, s1 = min(a.M, s0 + kQueriesPerWave);
+                if (s0 >= s1) continue;
+                bool any, all;
+                classify_mask_slice(a.mask, a.mask_qbs, a.mask_kbs, a.mask_qb, a.mask_kb, a.causal, s0, s1,
+                                    k0, k1, any, all);
+                any_bits |= (any ? 1u : 0u) << w;
+                full_bits |= (all ? 1u : 0u) << w;
+            }
+        }
+        const unsigned long long bal = __ballot(any_bits != 0);
+        if (lane == 0) wave_counts[wave] = __popcll(bal);
+        __syncthreads();
+        int before = count, total = count;
+#pragma unroll
+        for (int w = 0; w < NWAVES; ++w) {
+            const int c = wave_counts[w];
+            before += w < wave ? c : 0;
+            total += c;
+        }
+        if (any_bits != 0) list[before + __popcll(bal & ((1ull << lane) - 1ull))] = list_entry(kt, any_bits, full_bits);
+        __syncthreads();  // wave_counts is rewritten in the next round
+        count = total;
+    }
+    return count;
+}
+
+// Stages of the LDS-list schedule: tiles it+1 .. it+NSTAGE-1 are in flight
+// while tile it is computed (three stages up to D = 64, two above, where a
+// stage is 32 KB or more).
+template <int D>
+constexpr int lds_list_stages() { return D <= 64 ? 3 : 2; }
+constexpr int kLdsListCountsBytes = 64;  // per-wavefront counts, then the list
+
+// Block-mask query tile with its list in LDS (one workgroup per query tile,
+// no key split): the list is built first (mask reads only, before any K/V
+// load), then the K/V tiles of its entries stream through a ring of
+// NSTAGE stages, NSTAGE-1 tiles ahead of the one being computed. The list is
+// read from LDS, so the only vector-memory operations in the loop are the
+// tile copies (2 CPT per thread and tile) and the wait before each barrier
+// leaves the younger tiles' copies in flight.
+template <typename W, int NWAVES, int MOD>
+__device__ __forceinline__ void lds_list_qtile(const FwdArgs& a, unsigned char* smem, int bh, int qt, int q0,
+                                               int wave) {
+    using L = typename W::L;
+    constexpr int D = L::CPR * 8;
+    constexpr int NSTAGE = lds_list_stages<D>();
+    constexpr int VM_PER_TILE = 2 * W::CPT;
+    static_assert(W::SN == W::BN, "one compute step per list entry");
+    lds_int* counts = (lds_int*)(smem + NSTAGE * L::STAGE);
+    lds_int* lst = counts + kLdsListCountsBytes / 4;
+    const int ntiles = build_tile_list_lds<NWAVES>(a, q0, W::BN, lst, counts);
+    W w(a, smem, bh, q0, wave);
+    if (ntiles == 0) {  // uniform over the workgroup
+        w.store_output();
+        return;
+    }
+    auto tile_of = [](int e) { return list_tile(e); };
+    w.copy_tile(tile_of(lst[0]), 0);
+    if (NSTAGE > 2 && ntiles > 1) {
+        w.copy_tile(tile_of(lst[1]), L::STAGE);
+        wait_vm<VM_PER_TILE>();  // tile 0 (and the Q fragments) landed; tile 1 in flight
+    } else {
+        wait_vm_loads();
+    }
+    w.zero_tail(tile_of(lst[0]), 0);
+    __syncthreads();
+    int stage = 0;
+    for (int it = 0; it < ntiles; ++it) {
+        const int ahead = it + NSTAGE - 1;  // tile copied during this step
+        int astage = stage + (NSTAGE - 1) * L::STAGE;
+        if (astage >= NSTAGE * L::STAGE) astage -= NSTAGE * L::STAGE;
+        if (ahead < ntiles) w.copy_tile(tile_of(lst[ahead]), astage);
+        const int e = lst[it];
+        if (w.tile_active(e)) {
+            if (MOD == MOD_PLAIN) __builtin_amdgcn_s_setprio(1);
+            w.qk(stage);
+            if (MOD == MOD_PLAIN) __builtin_amdgcn_s_setprio(0);
+            w.softmax(e);
+            if (MOD == MOD_PLAIN) __builtin_amdgcn_s_setprio(1);
+            w.pv(stage);
+            if (MOD == MOD_PLAIN) __builtin_amdgcn_s_setprio(0);
+        }
+        // tile it+1 must have landed; the copies of tile it+2 may stay in flight
+        if (NSTAGE > 2 && it + 2 < ntiles) wait_vm<VM_PER_TILE>();
+        else wait_vm_loads();
+        int nstage = stage + L::STAGE;
+        if (nstage >= NSTAGE * L::STAGE) nstage = 0;
+        if (it + 1 < ntiles) w.zero_tail(tile_of(lst[it + 1]), nstage);
+        __syncthreads();
+        stage = nstage;
+    }
+    w.store_output();
+}
+
 template <typename T, int D, int MOD, bool LIST, int NWAVES, int BN, int SB, bool SPLIT>
 __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* smem, int bh, int qt,
                                                int split = 0) {
@@ -1040,6 +1163,12 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
         finish_qtile<W, NTHREADS, SPLIT>(a, w, smem, bh, qt, q0, BLOCK_M, split, active);
         return;
     }
+    if constexpr (LIST) {
+        if (a.tile_counts == nullptr) {  // list built in LDS (no key split)
+            lds_list_qtile<W, NWAVES, MOD>(a, smem, bh, qt, q0, wave);
+            return;
+        }
+    }
     int ntiles;
     const int* list;
     tile_range(a, qt, BLOCK_M, BN, ntiles, list);
@@ -1089,7 +1218,10 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
 template <typename T, int D, int MOD, bool LIST, int NWAVES, bool PAIRED, int BN = kBlockN16, int SB = 1>
 __global__ __launch_bounds__(NWAVES * 64, (D == 256 ? 4 : 8) / NWAVES) void flash_fwd_lockstep_kernel(FwdArgs a) {
     using L = TileLayout<D, BN * SB>;
-    __shared__ __attribute__((aligned(16))) unsigned char smem[2 * L::STAGE];
+    // block-mask kernels: LDS sized at launch (list_kernel_lds_bytes)
+    extern __shared__ __attribute__((aligned(16))) unsigned char dyn_smem[];
+    __shared__ __attribute__((aligned(16))) unsigned char st_smem[LIST ? 16 : 2 * L::STAGE];
+    unsigned char* smem = LIST ? dyn_smem : st_smem;
     int bh, qts[2];
     if (!PAIRED) {  // key split s: workgroups [s * tiles, (s+1) * tiles)
         const int tiles = a.B * a.H * a.num_q_tiles;
@@ -1378,10 +1510,10 @@ __global__ __launch_bounds__(256) void combine_splits_kernel(FwdArgs a, int rows
 }
 
 template <typename K>
-hipError_t launch(K kernel, int threads, const FwdArgs& a, hipStream_t s, bool paired = false) {
+hipError_t launch(K kernel, int threads, const FwdArgs& a, hipStream_t s, bool paired = false, size_t lds = 0) {
     const int64_t grid = (int64_t)a.B * a.H * (paired ? (a.num_q_tiles + 1) / 2 : a.num_q_tiles) * a.num_splits;
     if (grid <= 0) return hipSuccess;
-    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(threads), 0, s, a);
+    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(threads), lds, s, a);
     return hipGetLastError();
 }
 
@@ -1409,13 +1541,35 @@ static int block_n16(int D, bool general_mod, bool tile_list) {
     return !general_mod ? kBlockN16Wide : kBlockN16;
 }
 
+// LDS of the 16-bit block-mask kernel (4 wavefronts, 64-key tiles): two
+// stages with the tile_list kernel's global list, or lds_list_stages stages,
+// the per-wavefront counts and the list itself with a list built in LDS.
+template <int D>
+static size_t list_kernel_lds_bytes_d(bool lds_list, int num_k_tiles) {
+    using L = TileLayout<D, kBlockN16>;
+    if (!lds_list) return 2 * (size_t)L::STAGE;
+    return (size_t)lds_list_stages<D>() * L::STAGE + kLdsListCountsBytes + 4 * (size_t)num_k_tiles;
+}
+
+size_t list_kernel_lds_bytes(int D, bool lds_list, int num_k_tiles) {
+    switch (D) {
+        case 32: return list_kernel_lds_bytes_d<32>(lds_list, num_k_tiles);
+        case 64: return list_kernel_lds_bytes_d<64>(lds_list, num_k_tiles);
+        case 128: return list_kernel_lds_bytes_d<128>(lds_list, num_k_tiles);
+        case 256: return list_kernel_lds_bytes_d<256>(lds_list, num_k_tiles);
+        default: return 0;
+    }
+}
+
 template <typename T, int D>
 static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
-    const bool list = a.tile_counts != nullptr;
+    const bool list = a.mask != nullptr;
     const bool paired = pairs_causal_tiles(a.causal != 0, list) && a.num_splits == 1;
-    if (list)
-        return general_mod ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, true, 4, false>, 256, a, s)
-                           : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, true, 4, false>, 256, a, s);
+    if (list) {
+        const size_t lds = list_kernel_lds_bytes(D, a.tile_counts == nullptr, a.num_k_tiles);
+        return general_mod ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, true, 4, false>, 256, a, s, false, lds)
+                           : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, true, 4, false>, 256, a, s, false, lds);
+    }
     if constexpr (D == 256) {
         if (general_mod)
             return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 4, true>, 256, a, s, true)

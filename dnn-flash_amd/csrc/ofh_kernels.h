@@ -92,6 +92,28 @@ __host__ __device__ inline int list_tile(int e) { return e >> 8; }
 __host__ __device__ inline bool list_any(int e, int slice) { return ((e >> slice) & 1) != 0; }
 __host__ __device__ inline bool list_full(int e, int slice) { return ((e >> (4 + slice)) & 1) != 0; }
 
+// Rows [q0,q1) x keys [k0,k1) of a block-mask call, already clipped to the
+// problem: any = some pair is allowed by the mask (blocks out of its range are
+// disallowed) and by the causal rule; all = the mask allows every pair (causal
+// masking is applied element-wise by the attention kernel either way).
+__device__ inline void classify_mask_slice(const uint8_t* mask, int qbs, int kbs, int nqb, int nkb, int causal,
+                                           int q0, int q1, int k0, int k1, bool& any, bool& all) {
+    any = false;
+    all = true;
+    const int qb0 = q0 / qbs, qb1 = (q1 - 1) / qbs;
+    const int kb0 = k0 / kbs, kb1 = (k1 - 1) / kbs;
+    for (int qb = qb0; qb <= qb1; ++qb) {
+        const int qe = min(q1, (qb + 1) * qbs);
+        for (int kb = kb0; kb <= kb1; ++kb) {
+            const int ks = max(k0, kb * kbs);
+            const bool allowed = qb < nqb && kb < nkb && mask[(int64_t)qb * nkb + kb] != 0;
+            // causal: some key of the block is <= some query of the block iff ks <= qe-1
+            any = any || (allowed && (!causal || ks <= qe - 1));
+            all = all && allowed;
+        }
+    }
+}
+
 struct TileListArgs {
     int M, N, block_m, block_n, causal;
     const uint8_t* mask;
@@ -131,6 +153,10 @@ hipError_t launch_qk_score(const QkScoreArgs& a, int dtype, hipStream_t s);
 bool qk_score_mfma_supported(const QkScoreArgs& a, int dtype);
 hipError_t launch_qk_score_mfma(const QkScoreArgs& a, int dtype, hipStream_t s);
 
+// LDS bytes of the 16-bit block-mask kernel: with lds_list the workgroup
+// builds its query tile's list in LDS (no tile_list launch, no workspace).
+size_t list_kernel_lds_bytes(int D, bool lds_list, int num_k_tiles);
+constexpr int kLdsListMaxTiles = 4096;  // key tiles of a list built in LDS
 // Head dims (D == Dv) the MFMA kernels are built for: 32, 64, 128 (fp32) and 256 (bf16/fp16).
 bool flash_mfma_head_dim(int dtype, int D);
 const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile_list);

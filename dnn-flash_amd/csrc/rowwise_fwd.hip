@@ -156,27 +156,6 @@ hipError_t launch_rowwise(const FwdArgs& a, int dtype, hipStream_t s) {
 // per-wavefront ballot and a prefix over the wavefronts' counts.
 namespace {
 
-// Rows [q0,q1) x keys [k0,k1), already clipped to the problem. any: some pair
-// is allowed by the mask and by the causal rule; all: the mask allows every pair.
-__device__ void classify_slice(const TileListArgs& a, int q0, int q1, int k0, int k1, bool& any,
-                               bool& all) {
-    any = false;
-    all = true;
-    const int qb0 = q0 / a.mask_qbs, qb1 = (q1 - 1) / a.mask_qbs;
-    const int kb0 = k0 / a.mask_kbs, kb1 = (k1 - 1) / a.mask_kbs;
-    for (int qb = qb0; qb <= qb1; ++qb) {
-        const int qe = min(q1, (qb + 1) * a.mask_qbs);
-        for (int kb = kb0; kb <= kb1; ++kb) {
-            const int ks = max(k0, kb * a.mask_kbs);
-            const bool allowed = qb < a.mask_qb && kb < a.mask_kb &&
-                                 a.mask[(int64_t)qb * a.mask_kb + kb] != 0;
-            // causal: some key of the block is <= some query of the block iff ks <= qe-1
-            any = any || (allowed && (!a.causal || ks <= qe - 1));
-            all = all && allowed;
-        }
-    }
-}
-
 constexpr int kListWaves = 4;
 
 __global__ __launch_bounds__(64 * kListWaves) void tile_list_kernel(TileListArgs a) {
@@ -196,7 +175,8 @@ __global__ __launch_bounds__(64 * kListWaves) void tile_list_kernel(TileListArgs
                 const int s0 = q0 + 32 * w, s1 = min(a.M, s0 + 32);
                 if (s0 >= s1) continue;
                 bool any, all;
-                classify_slice(a, s0, s1, k0, k1, any, all);
+                classify_mask_slice(a.mask, a.mask_qbs, a.mask_kbs, a.mask_qb, a.mask_kb, a.causal, s0, s1,
+                                    k0, k1, any, all);
                 any_bits |= (any ? 1u : 0u) << w;
                 full_bits |= (all ? 1u : 0u) << w;
             }

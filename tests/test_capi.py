@@ -265,8 +265,16 @@ def test_workspace_bytes(ofh):
     mk = dict(mask_allowed=m.ctypes.data, mask_query_block_size=64, mask_key_block_size=64,
               mask_query_blocks=8, mask_key_blocks=8)
     p = F.make_params(1, 1, 512, 512, 64, dtype=F.DTYPE_BF16, max_key_splits=1, **mk)
+    assert F.workspace_bytes(p) == 0  # each workgroup builds its list in LDS
     nqt, nkt = 4, 8  # 128-row query tiles (block-mask schedule), 64-key tiles
+    # fp32, or more than 4096 key tiles: lists built by the tile_list kernel in the workspace
+    p = F.make_params(1, 1, 512, 512, 64, dtype=F.DTYPE_F32, max_key_splits=1, **mk)
     assert F.workspace_bytes(p) == 256 + nqt * nkt * 4
+    mbig = np.ones((1, 4097), np.uint8)
+    p = F.make_params(1, 1, 64, 4097 * 64, 64, dtype=F.DTYPE_BF16, max_key_splits=1,
+                      mask_allowed=mbig.ctypes.data, mask_query_block_size=64, mask_key_block_size=64,
+                      mask_query_blocks=1, mask_key_blocks=4097)
+    assert F.workspace_bytes(p) == 256 + 4097 * 4
     p = F.make_params(1, 1, 512, 512, 64, dtype=F.DTYPE_BF16, **mk)
     splits = F.launch_info(p).key_splits
     assert splits == 8

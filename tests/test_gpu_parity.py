@@ -149,6 +149,34 @@ def test_block_mask_long_key_ranges(ofh, dt):
                   f"{dt} block mask M{M} N{N} causal={causal}")
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_block_mask_global_list(ofh, dt):
+    """More key tiles than a workgroup's LDS list holds (4096): the lists are
+    built by the tile_list kernel in the workspace and read from global
+    memory; sampled rows against the row oracle."""
+    F = ofh
+    B, H, M, N, D = 1, 1, 200, 4200 * 64, 64
+    rng = np.random.default_rng(5)
+    qb, kb = -(-M // 64), N // 64
+    mask = (rng.random((qb, kb)) < 0.05).astype(np.uint8)
+    mask[:, 0] = 1
+    mask[:, kb - 30:] = 1
+    dev, host = make_inputs(dt, B, H, M, N, D, seed=77)
+    code = {"bf16": F.DTYPE_BF16, "f16": F.DTYPE_F16}[dt]
+    tmask = torch.from_numpy(mask).cuda()
+    p = F.make_params(B, H, M, N, D, dtype=code, max_key_splits=1, mask_allowed=tmask.data_ptr(),
+                      mask_query_block_size=64, mask_key_block_size=64, mask_query_blocks=qb,
+                      mask_key_blocks=kb)
+    assert F.workspace_bytes(p) > 0
+    for causal in (False, True):
+        out = run(ofh, dev, dt=dt, causal=causal, mask=mask, mbs=(64, 64), max_key_splits=1)
+        rows = np.arange(0, M, 7, dtype=np.uint64)
+        prob = O.Problem(B, H, M, N, D, D, scale=1.0 / math.sqrt(D), causal=causal, mask=mask,
+                         mask_query_block_size=64, mask_key_block_size=64)
+        ref = O.standard_attention_rows(*host, prob, np.zeros(len(rows), np.uint64), rows, threads=THREADS)
+        check(out[0, 0, rows.astype(np.int64)], ref, dt, f"{dt} global list N{N} causal={causal}")
+
+
 def test_fully_masked_rows_are_zero(ofh):
     M, N, D = 256, 256, 128
     dev, host = make_inputs("bf16", 1, 2, M, N, D, seed=12)

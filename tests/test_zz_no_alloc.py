@@ -48,8 +48,9 @@ def test_noalloc_matches_fwd(ofh):
     F = ofh
     lib = F.lib()
     cases = [  # (label, dtype, B, H, M, N, D, causal, block mask?, max_key_splits)
-        ("bf16 block mask", "bf16", 1, 4, 4096, 4096, 64, True, True, 1),
-        ("bf16 block mask, smaller", "bf16", 1, 2, 1024, 1024, 64, True, True, 1),
+        ("bf16 block mask, list in LDS (no scratch)", "bf16", 1, 4, 4096, 4096, 64, True, True, 1),
+        ("fp32 block mask", "f32", 1, 4, 2048, 2048, 64, True, True, 1),
+        ("fp32 block mask, smaller", "f32", 1, 2, 1024, 1024, 64, True, True, 1),
         ("bf16 key split", "bf16", 1, 2, 64, 16384, 128, False, False, 0),
         ("bf16 key split, smaller", "bf16", 1, 1, 1, 4000, 128, False, False, 0),  # merged in the launch
         ("fp32 key split", "f32", 1, 4, 256, 1024, 64, False, False, 0),
@@ -73,7 +74,7 @@ def test_noalloc_matches_fwd(ofh):
                           causal=causal, max_key_splits=splits, **kw)
         assert (F.launch_info(p).key_splits > 1) == ("key split" in label), label
         need = F.workspace_bytes(p)
-        assert 0 < need <= NOALLOC_MAX, (label, need)
+        assert need <= NOALLOC_MAX and (need == 0) == ("no scratch" in label), (label, need)
         o_ref = torch.empty((B, H, M, D), device="cuda", dtype=torch.float32)
         o_na = torch.full_like(o_ref, float("nan"))
         torch.cuda.synchronize()
