@@ -60,6 +60,38 @@ void validate_mask(const BlockMask& m) {
 
 size_t round_up(size_t x) { return (x + 255) & ~size_t(255); }
 
+// Dense fp32 bias [M, N] for a host score_bias callback, shared by every head:
+// the callback runs once per pair that the causal rule and the block mask let
+// through, the pairs the reference evaluates it for (masked_out before the
+// bias, attention.cpp:101-107); masked pairs hold 0 and are never used. The
+// array is staged to the device, so its size is capped at kMaxHostBiasBytes.
+constexpr size_t kMaxHostBiasBytes = size_t(1) << 31;
+
+std::vector<float> expand_score_bias(const AttentionOptions& o, size_t M, size_t N) {
+    std::vector<float> dense;
+    if (!o.score_bias) return dense;
+    if (M > kMaxHostBiasBytes / 4 / N)
+        throw std::invalid_argument("score_bias: the dense [" + std::to_string(M) + " x " + std::to_string(N) +
+                                    "] fp32 bias exceeds 2 GiB; use alibi_slopes or the C API with a "
+                                    "device bias tensor");
+    dense.assign(M * N, 0.0f);
+    const BlockMask* bm = o.block_mask;  // validated by the caller
+    for (size_t i = 0; i < M; ++i) {
+        const size_t jend = o.causal ? std::min(N, i + 1) : N;
+        const size_t qb = bm ? i / bm->query_block_size : 0;
+        if (bm && qb >= bm->query_blocks) continue;  // the whole row is masked
+        float* row = dense.data() + i * N;
+        for (size_t j = 0; j < jend; ++j) {
+            if (bm) {
+                const size_t kb = j / bm->key_block_size;
+                if (kb >= bm->key_blocks || bm->allowed[qb * bm->key_blocks + kb] == 0) continue;
+            }
+            row[j] = o.score_bias(i, j);
+        }
+    }
+    return dense;
+}
+
 // One fp32 attention call on host tensors [B*H, T, *] through `ws`.
 void run_host(const float* q, const float* k, const float* v, float* out, size_t B, size_t H,
               const AttentionShape& s, const AttentionOptions& o, int algorithm,
@@ -75,13 +107,7 @@ void run_host(const float* q, const float* k, const float* v, float* out, size_t
     if (!o.alibi_slopes.empty() && o.alibi_slopes.size() != H)
         throw std::invalid_argument("alibi_slopes must hold one slope per head");
 
-    std::vector<float> dense;
-    if (o.score_bias) {
-        // Host callback: evaluated once per (query, key), shared by every head.
-        dense.resize(M * N);
-        for (size_t i = 0; i < M; ++i)
-            for (size_t j = 0; j < N; ++j) dense[i * N + j] = o.score_bias(i, j);
-    }
+    const std::vector<float> dense = expand_score_bias(o, M, N);
 
     const size_t nq = B * H * M * D, nk = B * H * N * D, nv = B * H * N * Dv, no = B * H * M * Dv;
     const size_t nmask = o.block_mask ? o.block_mask->allowed.size() : 0;
@@ -300,12 +326,7 @@ void flash_attention_batched_device(const void* q, const void* k, const void* v,
     if (!o.alibi_slopes.empty() && o.alibi_slopes.size() != shape.heads)
         throw std::invalid_argument("alibi_slopes must hold one slope per head");
     const size_t M = shape.query_tokens, N = shape.key_tokens;
-    std::vector<float> dense;
-    if (o.score_bias) {
-        dense.resize(M * N);
-        for (size_t i = 0; i < M; ++i)
-            for (size_t j = 0; j < N; ++j) dense[i * N + j] = o.score_bias(i, j);
-    }
+    const std::vector<float> dense = expand_score_bias(o, M, N);
     const size_t nmask = o.block_mask ? o.block_mask->allowed.size() : 0;
     const size_t off_b = round_up(nmask), off_s = off_b + round_up(dense.size() * 4);
     const size_t total = off_s + round_up(o.alibi_slopes.size() * 4);

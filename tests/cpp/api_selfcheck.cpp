@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <cstring>
 #include <stdexcept>
+#include <string>
 #include <vector>
 
 #include "onednn_flash/attention.hpp"
@@ -208,6 +209,36 @@ int main() {
     const auto fl_mask = of::flash_attention_tiled(q, k, v, shape, mopts);
     expect(of::max_abs_diff(std_mask, fl_mask) <= 1e-5f, "block mask + score_bias: flash vs standard",
            of::max_abs_diff(std_mask, fl_mask));
+    {   // the callback runs only for pairs that the block mask and the causal rule let through
+        size_t calls = 0, masked_calls = 0;
+        auto copts = mopts;
+        copts.causal = true;
+        copts.score_bias = [&](std::size_t qi, std::size_t kj) {
+            ++calls;
+            if (kj > qi || !bm.allows(qi, kj)) ++masked_calls;
+            return 0.0f;
+        };
+        (void)of::flash_attention_tiled(q, k, v, shape, copts);
+        size_t unmasked = 0;
+        for (std::size_t qi = 0; qi < shape.query_tokens; ++qi)
+            for (std::size_t kj = 0; kj <= qi && kj < shape.key_tokens; ++kj) unmasked += bm.allows(qi, kj) ? 1 : 0;
+        expect(masked_calls == 0 && calls == unmasked, "score_bias evaluated on unmasked pairs only",
+               (float)masked_calls);
+        // a dense bias beyond 2 GiB is refused before any device work
+        of::AttentionShape big = shape;
+        big.query_tokens = big.key_tokens = 32768;
+        auto bopts = options;
+        bopts.score_bias = [](std::size_t, std::size_t) { return 0.0f; };
+        bool refused = false;
+        try {
+            (void)of::flash_attention_tiled(std::vector<float>(big.query_tokens * big.head_dim),
+                                            std::vector<float>(big.key_tokens * big.head_dim),
+                                            std::vector<float>(big.key_tokens * big.value_dim), big, bopts);
+        } catch (const std::invalid_argument& e) {
+            refused = std::string(e.what()).find("exceeds 2 GiB") != std::string::npos;
+        }
+        expect(refused, "score_bias over 2 GiB refused", 0.0f);
+    }
     auto aopts = options;
     aopts.block_mask = &bm;
     aopts.alibi_slopes = {0.25f};
