@@ -714,14 +714,17 @@ struct Wave32 {
 
     // Scores in log2 units with the call's score_mod: scale, then ALiBi
     // slope*(key - query) or a dense bias, then cap*tanh(x/cap). Constants are
-    // folded so ALiBi costs two FMAs per score and the soft-cap an exp2, a
-    // reciprocal and two more VALU operations:
-    //   u = 2 log2e t / cap, tanh = 1 - 2/(2^u + 1), x = log2e cap tanh.
+    // folded so ALiBi costs two FMAs per score and the soft-cap an exp2, an
+    // add and a reciprocal:
+    //   u = 2 log2e t / cap, tanh = 1 - 2/(2^u + 1), x = log2e cap tanh
+    //     = cap_hi + cap_m2 * r with r = 1/(2^u + 1), cap_hi = log2e cap,
+    //   cap_m2 = -2 log2e cap < 0;
+    // with a soft-cap s is left holding r (the softmax takes the row max from
+    // min r and folds cap_hi + cap_m2 * r into its exp2 argument).
     template <int BIAS, bool CAP>
     __device__ __forceinline__ void score_mod_tile(int k0) {
         const float c_s = CAP ? a.scale * (2.0f * kLog2e) * a.inv_softcap : a.scale_log2;
         const float c_b = CAP ? (2.0f * kLog2e) * a.inv_softcap : kLog2e;
-        const float cap_hi = a.softcap * kLog2e, cap_m2 = -2.0f * a.softcap * kLog2e;
         const float sl = slope * c_b;
         const float base = sl * (float)(k0 + 8 * g - my_q);
         float bvals[BN / 2];
@@ -753,8 +756,9 @@ struct Wave32 {
                     u = __builtin_fmaf(s[sb][e], c_s, bvals[16 * sb + e] * c_b);
                 else
                     u = s[sb][e] * c_s;
-                if (CAP)
-                    u = __builtin_fmaf(cap_m2, __builtin_amdgcn_rcpf(__builtin_amdgcn_exp2f(u) + 1.0f), cap_hi);
+                // with a soft-cap, s keeps r = 1 / (2^u + 1): the log2 score is
+                // cap_hi + cap_m2 * r, formed inside the softmax's exp2 argument
+                if (CAP) u = __builtin_amdgcn_rcpf(__builtin_amdgcn_exp2f(u) + 1.0f);
                 s[sb][e] = u;
             }
     }
@@ -772,9 +776,10 @@ struct Wave32 {
         }
     }
 
-    // Masked scores -> -inf. Causal / ragged end: key k0+8g+pos is valid iff
-    // pos < lim. With a block mask whose blocks cut the slice: per element.
-    __device__ __forceinline__ void apply_mask(int e_ent, int k0) {
+    // Masked scores -> `masked` (-inf, or +inf for soft-capped scores held as
+    // r). Causal / ragged end: key k0+8g+pos is valid iff pos < lim. With a
+    // block mask whose blocks cut the slice: per element.
+    __device__ __forceinline__ void apply_mask(int e_ent, int k0, float masked = kNegInf) {
         if (LIST && !list_full(e_ent, wave)) {
             // masked_out (attention.cpp:54-62) per element, branch-free: the
             // bitmap bytes are read at clamped indices and combined by selects
@@ -797,7 +802,7 @@ struct Wave32 {
                 for (int t = 0; t < 8; ++t) {
                     const int kj = k0 + 8 * g + tile_pos(sb, e0 + t);
                     const bool ok = row_ok & (kj <= klim) & (kbs[t] < a.mask_kb) & (byte[t] != 0);
-                    s[sb][e0 + t] = ok ? s[sb][e0 + t] : kNegInf;
+                    s[sb][e0 + t] = ok ? s[sb][e0 + t] : masked;
                 }
             }
             return;
@@ -807,7 +812,7 @@ struct Wave32 {
         for (int sb = 0; sb < BN / 32; ++sb)
 #pragma unroll
             for (int e = 0; e < 16; ++e)
-                if (tile_pos(sb, e) >= lim) s[sb][e] = kNegInf;
+                if (tile_pos(sb, e) >= lim) s[sb][e] = masked;
     }
 
     // Online softmax of the scores in s (tile step with entry e_ent): running
@@ -818,6 +823,8 @@ struct Wave32 {
         const bool need_mask = tile_crosses(kt) || (LIST && !list_full(e_ent, wave));
         float mx = kNegInf;
         const bool raw = MOD == MOD_PLAIN && !need_mask;  // s still holds raw dot products
+        const bool capped = MOD == MOD_GENERAL && a.softcap > 0.0f;  // uniform
+        const float cap_hi = a.softcap * kLog2e, cap_m2 = -2.0f * a.softcap * kLog2e;
         if (raw) {
             if (a.scale_log2 >= 0.0f) {
 #pragma unroll
@@ -833,6 +840,15 @@ struct Wave32 {
                     for (int e = 0; e < 16; ++e) mn = fminf(mn, s[sb][e]);
                 mx = mn * a.scale_log2;
             }
+        } else if (capped) {
+            general_scores(k0);  // s = r, log2 score cap_hi + cap_m2 * r, decreasing in r
+            if (need_mask) apply_mask(e_ent, k0, __builtin_huge_valf());
+            float mn = __builtin_huge_valf();
+#pragma unroll
+            for (int sb = 0; sb < BN / 32; ++sb)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) mn = fminf(mn, s[sb][e]);
+            mx = __builtin_fmaf(mn, cap_m2, cap_hi);  // -inf when every score is masked
         } else {
             if (MOD == MOD_GENERAL) {
                 general_scores(k0);
@@ -868,6 +884,13 @@ struct Wave32 {
                 for (int t = 0; t < 8; ++t)
                     pf[c][t] = (T)__builtin_amdgcn_exp2f(
                         __builtin_fmaf(s[c >> 1][8 * (c & 1) + t], a.scale_log2, -m_use));
+        } else if (capped) {
+            const float c0 = cap_hi - m_use;
+#pragma unroll
+            for (int c = 0; c < BN / 16; ++c)
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+                    pf[c][t] = (T)__builtin_amdgcn_exp2f(__builtin_fmaf(s[c >> 1][8 * (c & 1) + t], cap_m2, c0));
         } else {
 #pragma unroll
             for (int c = 0; c < BN / 16; ++c)
