@@ -211,8 +211,8 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
                          std::llabs((long long)r.ks[2]) <= (1 << 24) && std::llabs((long long)r.vs[2]) <= (1 << 24);
     if (p->algorithm == OFH_ALGO_FLASH_MFMA && !mfma_ok)
         return set_error(OFH_ERROR_UNSUPPORTED,
-                         "flash MFMA kernel needs head_dim == value_dim in {32, 64, 128} (and 256 for "
-                         "bf16/fp16), 16-byte "
+                         "flash MFMA kernel needs head_dim == value_dim in {32, 64, 96, 128} (fp32) or a "
+                         "multiple of 32 up to 256 (bf16/fp16), 16-byte "
                          "aligned rows and K/V token strides of at most 2^24 elements; use "
                          "OFH_ALGO_AUTO or OFH_ALGO_ROWWISE");
     if (p->algorithm == OFH_ALGO_ROWWISE || !mfma_ok) {

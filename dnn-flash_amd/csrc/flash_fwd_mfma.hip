@@ -465,11 +465,17 @@ __device__ __forceinline__ void dma16(const void* g, unsigned lds) {
 // K fragments read rows kappa(0..15) at one chunk per 16 lanes; V^T fragments
 // are transposing reads of 4 rows x 2 chunks per 16 lanes. For D = 64 two rows
 // share a 256-byte bank line, hence row >> 1.
+//
+// Head dims that are not powers of two (96, 160, 192, 224) keep rows
+// unswizzled: chunk c of row r at position c, read at offset + 32c (K) and
+// + 64 db (V) instead of an XOR (their rows are not a power-of-two number of
+// chunks, so an XOR could leave the row).
 template <int D, int BN>
 struct TileLayout {
     static constexpr int RB = D * 2;              // bytes of one K/V row
     static constexpr int CPR = D / 8;             // 16-byte chunks per row
-    static_assert(D == 32 || D == 64 || D == 128 || D == 256, "head dims of the 16-bit kernels");
+    static constexpr bool POW2 = (D & (D - 1)) == 0;
+    static_assert(D % 32 == 0 && D >= 32 && D <= 256, "head dims of the 16-bit kernels: multiples of 32 up to 256");
     // Both swizzles must repeat every 8 rows or less at D = 256 (every 16 at
     // D = 128, 32 at D = 64, 64 at D = 32): a copy lane reuses one swizzled
     // chunk offset for the rows DSTEP = 64 * wavefronts / CPR apart that it
@@ -477,12 +483,14 @@ struct TileLayout {
     // repeat every 4 rows: a V^T fragment is two transposing reads 4 rows
     // apart at one lane offset.
     static __device__ __forceinline__ int kswz(int row) {
+        if (!POW2) return 0;
         if (D == 256) return row & 7;
         if (D == 128) return row & 15;
         if (D == 64) return (row >> 1) & 7;
         return (row >> 2) & 3;  // D = 32: four rows share a bank line
     }
     static __device__ __forceinline__ int vswz(int row) {
+        if (!POW2) return 0;
         if (D >= 128) return 4 * (row & 3);
         if (D == 64) return 4 * ((row >> 1) & 1);
         return 0;  // D = 32: a row is one 32-column block
@@ -536,8 +544,7 @@ struct Wave32 {
     static constexpr int BN = BN_;
     static constexpr int SN = BN_ * SB;                 // keys per staged tile
     static constexpr int CPT = SN * L::CPR / NTHREADS;  // 16-byte chunks per thread per tile
-    static_assert(CPT >= 1 && SN * L::CPR % NTHREADS == 0 && NTHREADS % L::CPR == 0,
-                  "tile must split evenly");
+    static_assert(CPT >= 1 && SN * L::CPR % NTHREADS == 0, "tile must split evenly");
 
     const FwdArgs& a;
     unsigned char* smem;
@@ -557,10 +564,19 @@ struct Wave32 {
     // LDS read lane offsets
     int k_lane_off, v_lane_off;
     // K/V copies: lane offsets (elements) of its chunk in rows dma_row0 + u*DSTEP
-    static constexpr int DSTEP = 64 * (NTHREADS / 64) / L::CPR;
-    static_assert(DSTEP % (D == 256 ? 8 : D == 128 ? 16 : D == 64 ? 32 : 64) == 0,
+    // when a copy instruction covers whole rows (64 * wavefronts divisible by
+    // the chunks per row: every power-of-two D); otherwise each instruction's
+    // row and chunk are derived from its slot index.
+    static constexpr bool UNIFORM_COPY = (64 * (NTHREADS / 64)) % L::CPR == 0;
+    static constexpr int DSTEP = UNIFORM_COPY ? 64 * (NTHREADS / 64) / L::CPR : 0;
+    static_assert(!UNIFORM_COPY || !L::POW2 ||
+                      DSTEP % (D == 256 ? 8 : D == 128 ? 16 : D == 64 ? 32 : 64) == 0,
                   "the K/V swizzles must repeat within the rows one copy lane covers");
+    static_assert(UNIFORM_COPY || !L::POW2, "unswizzled rows when an instruction splits a row");
     int dma_row0, dma_koff, dma_voff;
+    // K fragment c (chunks 2c, 2c+1) and V^T block db at the lane's read offsets
+    __device__ __forceinline__ int k_off(int c) const { return L::POW2 ? (k_lane_off ^ (32 * c)) : k_lane_off + 32 * c; }
+    __device__ __forceinline__ int v_off(int db) const { return L::POW2 ? (v_lane_off ^ (64 * db)) : v_lane_off + 64 * db; }
 
     __device__ __forceinline__ Wave32(const FwdArgs& args, unsigned char* sm, int bh, int q0, int wv)
         : a(args), smem(sm), wave(wv) {
@@ -631,6 +647,18 @@ struct Wave32 {
         const T* vt_base = Vp + (int64_t)k0 * a.v_sn;
         const unsigned lds0 = (unsigned)(uintptr_t)smem + stage_off + 1024 * wave;
         constexpr int NW = NTHREADS / 64;
+        if constexpr (!UNIFORM_COPY) {
+            // slot 64 (u NW + wave) + lane: row slot / CPR, chunk slot % CPR (unswizzled)
+#pragma unroll
+            for (int u = 0; u < CPT; ++u) {
+                const int slot = 64 * (u * NW + wave) + (tid & 63);
+                const int row = slot / L::CPR, pos = slot - row * L::CPR;
+                const int rr = min(k0 + row, a.N - 1) - k0;
+                dma16(kt_base + (int64_t)rr * a.k_sn + 8 * pos, lds0 + 1024 * NW * u);
+                dma16(vt_base + (int64_t)rr * a.v_sn + 8 * pos, lds0 + L::KTILE + 1024 * NW * u);
+            }
+            return;
+        }
         if (k0 + SN <= a.N) {
             const T* kp = kt_base + dma_koff;
             const T* vp = vt_base + dma_voff;
@@ -657,9 +685,11 @@ struct Wave32 {
         constexpr int NW = NTHREADS / 64;
         const u32x4 zero = {0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int u = 0; u < CPT; ++u)
-            if (k0 + dma_row0 + u * DSTEP >= a.N)
+        for (int u = 0; u < CPT; ++u) {
+            const int row = UNIFORM_COPY ? dma_row0 + u * DSTEP : (64 * (u * NW + wave) + (tid & 63)) / L::CPR;
+            if (k0 + row >= a.N)
                 *(u32x4*)(smem + stage_off + L::KTILE + 1024 * wave + 1024 * NW * u + 16 * (tid & 63)) = zero;
+        }
     }
 
     // S^T = K Q^T for the tile in LDS stage `stage_off`.
@@ -671,7 +701,7 @@ struct Wave32 {
         const lds_u8* kbs = (const lds_u8*)smem + stage_off + sub * BN * L::KSTR;
         auto rd = [&](int i) {
             const int sb = i / (D / 16), c = i % (D / 16);
-            return __builtin_bit_cast(v8, *(const lds_u32x4*)(kbs + 32 * sb * L::KSTR + (k_lane_off ^ (32 * c))));
+            return __builtin_bit_cast(v8, *(const lds_u32x4*)(kbs + 32 * sb * L::KSTR + k_off(c)));
         };
         v8 f[kFragAhead];
 #pragma unroll
@@ -692,7 +722,7 @@ struct Wave32 {
     __device__ __forceinline__ void pv(int stage_off, int sub = 0) {
         const lds_u8* vbs = (const lds_u8*)smem + stage_off + sub * BN * L::VSTR;
         auto vfrag = [&](int c, int db) {
-            const int off = v_lane_off ^ (64 * db);
+            const int off = v_off(db);
             const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vbs + (16 * c) * L::VSTR + off));
             const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vbs + (16 * c + 4) * L::VSTR + off));
             return __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -1236,10 +1266,13 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
     finish_qtile<W, NTHREADS, SPLIT>(a, w, smem, bh, qt, q0, BLOCK_M, split, active);
 }
 
-// D = 256 runs one 4-wavefront workgroup per CU (one wavefront per SIMD, so
-// the O accumulators can use the accumulation registers).
+// Workgroups per CU the register budget is sized for: one of 8 wavefronts,
+// two of 4, or one of 4 from D = 160 up (one wavefront per SIMD, so the O
+// accumulators can use the accumulation registers).
+constexpr int lockstep_min_blocks(int D, int nwaves) { return nwaves == 8 ? 1 : (D >= 160 ? 1 : 2); }
+
 template <typename T, int D, int MOD, bool LIST, int NWAVES, bool PAIRED, int BN = kBlockN16, int SB = 1>
-__global__ __launch_bounds__(NWAVES * 64, (D == 256 ? 4 : 8) / NWAVES) void flash_fwd_lockstep_kernel(FwdArgs a) {
+__global__ __launch_bounds__(NWAVES * 64, lockstep_min_blocks(D, NWAVES)) void flash_fwd_lockstep_kernel(FwdArgs a) {
     using L = TileLayout<D, BN * SB>;
     // block-mask kernels: LDS sized at launch (list_kernel_lds_bytes)
     extern __shared__ __attribute__((aligned(16))) unsigned char dyn_smem[];
@@ -1556,11 +1589,12 @@ static bool pairs_causal_tiles(bool causal, bool tile_list) { return causal && !
 // step (+9 to +13 %); at D = 128, where S and P for 128 keys would spill, they
 // are computed in two 64-key steps between the same barriers (+1 to +5 %).
 // D = 32 stages 128 keys in every kernel without a block mask (a 64-key tile
-// of 64-byte rows is fewer 16-byte chunks than the 8 wavefronts copy), and
-// D = 256 runs 4 wavefronts (128 query rows) on 64-key tiles throughout.
+// of 64-byte rows is fewer 16-byte chunks than the 8 wavefronts copy), as do
+// D = 96 and 160 (their 64-key tiles do not split evenly over 512 threads);
+// D > 160 runs 4 wavefronts (128 query rows) on 64-key tiles throughout.
 static int block_n16(int D, bool general_mod, bool tile_list) {
-    if (D == 256 || tile_list) return kBlockN16;
-    if (D == 32) return kBlockN16Wide;
+    if (D > 160 || tile_list) return kBlockN16;
+    if (D == 32 || D == 96 || D == 160) return kBlockN16Wide;
     return !general_mod ? kBlockN16Wide : kBlockN16;
 }
 
@@ -1578,7 +1612,11 @@ size_t list_kernel_lds_bytes(int D, bool lds_list, int num_k_tiles) {
     switch (D) {
         case 32: return list_kernel_lds_bytes_d<32>(lds_list, num_k_tiles);
         case 64: return list_kernel_lds_bytes_d<64>(lds_list, num_k_tiles);
+        case 96: return list_kernel_lds_bytes_d<96>(lds_list, num_k_tiles);
         case 128: return list_kernel_lds_bytes_d<128>(lds_list, num_k_tiles);
+        case 160: return list_kernel_lds_bytes_d<160>(lds_list, num_k_tiles);
+        case 192: return list_kernel_lds_bytes_d<192>(lds_list, num_k_tiles);
+        case 224: return list_kernel_lds_bytes_d<224>(lds_list, num_k_tiles);
         case 256: return list_kernel_lds_bytes_d<256>(lds_list, num_k_tiles);
         default: return 0;
     }
@@ -1593,15 +1631,15 @@ static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
         return general_mod ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, true, 4, false>, 256, a, s, false, lds)
                            : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, true, 4, false>, 256, a, s, false, lds);
     }
-    if constexpr (D == 256) {
+    if constexpr (D > 160) {
         if (general_mod)
             return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 4, true>, 256, a, s, true)
                           : launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 4, false>, 256, a, s);
         return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 4, true>, 256, a, s, true)
                       : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 4, false>, 256, a, s);
     } else {
-        // score_mod: 64-key compute steps (two per staged tile at D = 32)
-        constexpr int GSB = D == 32 ? 2 : 1;
+        // score_mod: 64-key compute steps (two per staged tile at D = 32, 96, 160)
+        constexpr int GSB = (D == 32 || (D & (D - 1)) != 0) ? 2 : 1;
         if (general_mod)
             return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8, true, kBlockN16, GSB>, 512, a, s, true)
                           : launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8, false, kBlockN16, GSB>, 512, a, s);
@@ -1614,17 +1652,23 @@ static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
 }
 
 hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipStream_t s) {
-    if (dtype == DT_BF16) {
-        if (a.D == 32) return launch16<__bf16, 32>(a, general_mod, s);
-        if (a.D == 64) return launch16<__bf16, 64>(a, general_mod, s);
-        if (a.D == 128) return launch16<__bf16, 128>(a, general_mod, s);
-        if (a.D == 256) return launch16<__bf16, 256>(a, general_mod, s);
-    } else if (dtype == DT_F16) {
-        if (a.D == 32) return launch16<_Float16, 32>(a, general_mod, s);
-        if (a.D == 64) return launch16<_Float16, 64>(a, general_mod, s);
-        if (a.D == 128) return launch16<_Float16, 128>(a, general_mod, s);
-        if (a.D == 256) return launch16<_Float16, 256>(a, general_mod, s);
+    if (dtype == DT_BF16 || dtype == DT_F16) {
+        const bool f16 = dtype == DT_F16;
+        switch (a.D) {
+            case 32: return f16 ? launch16<_Float16, 32>(a, general_mod, s) : launch16<__bf16, 32>(a, general_mod, s);
+            case 64: return f16 ? launch16<_Float16, 64>(a, general_mod, s) : launch16<__bf16, 64>(a, general_mod, s);
+            case 96: return f16 ? launch16<_Float16, 96>(a, general_mod, s) : launch16<__bf16, 96>(a, general_mod, s);
+            case 128: return f16 ? launch16<_Float16, 128>(a, general_mod, s) : launch16<__bf16, 128>(a, general_mod, s);
+            case 160: return f16 ? launch16<_Float16, 160>(a, general_mod, s) : launch16<__bf16, 160>(a, general_mod, s);
+            case 192: return f16 ? launch16<_Float16, 192>(a, general_mod, s) : launch16<__bf16, 192>(a, general_mod, s);
+            case 224: return f16 ? launch16<_Float16, 224>(a, general_mod, s) : launch16<__bf16, 224>(a, general_mod, s);
+            case 256: return f16 ? launch16<_Float16, 256>(a, general_mod, s) : launch16<__bf16, 256>(a, general_mod, s);
+            default: return hipErrorInvalidValue;
+        }
     } else if (dtype == DT_F32) {
+        if (a.D == 96)
+            return general_mod ? launch(flash_fwd_mfma32_kernel<96, true, kTilesF32>, kThreads32, a, s)
+                               : launch(flash_fwd_mfma32_kernel<96, false, kTilesF32>, kThreads32, a, s);
         if (a.D == 32)
             return general_mod ? launch(flash_fwd_mfma32_kernel<32, true, kTilesF32>, kThreads32, a, s)
                                : launch(flash_fwd_mfma32_kernel<32, false, kTilesF32>, kThreads32, a, s);
@@ -1683,18 +1727,18 @@ hipError_t split_counter_slot(int slot, unsigned** ptr) {
 }
 
 bool flash_mfma_head_dim(int dtype, int D) {
-    if (dtype == DT_F32) return D == 32 || D == 64 || D == 128;
-    return D == 32 || D == 64 || D == 128 || D == 256;
+    if (dtype == DT_F32) return D == 32 || D == 64 || D == 96 || D == 128;
+    return D % 32 == 0 && D >= 32 && D <= 256;
 }
 
 const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile_list) {
     if (dtype < 0 || dtype > 2 || !flash_mfma_head_dim(dtype, D)) return "none";
-    // [dtype][log2(D) - 5][score_mod][list]
+    // [dtype][D / 32 - 1][score_mod][list]
     static const std::vector<std::string> names = [] {
         std::vector<std::string> v;
         const char* tn[3] = {"f32", "bf16", "f16"};
         for (int dt = 0; dt < 3; ++dt)
-            for (int d = 32; d <= 256; d *= 2)
+            for (int d = 32; d <= 256; d += 32)
                 for (int mod = 0; mod < 2; ++mod)
                     for (int list = 0; list < 2; ++list) {
                         std::string n;
@@ -1703,26 +1747,27 @@ const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile
                         } else {
                             n = std::string("flash_fwd_lockstep_kernel<") + tn[dt] + "," + std::to_string(d) +
                                 (mod ? ",mod" : ",plain");
+                            const bool pow2 = (d & (d - 1)) == 0;
                             if (list) n += ",list,4w>";
-                            else if (d == 256) n += ",4w>";
+                            else if (d > 160) n += ",4w>";
                             else if (!mod && d <= 64) n += ",8w,128keys>";
-                            else if (!mod && d == 128) n += ",8w,2x64keys>";
-                            else if (mod && d == 32) n += ",8w,2x64keys>";
+                            else if (!mod) n += ",8w,2x64keys>";
+                            else if (d == 32 || !pow2) n += ",8w,2x64keys>";
                             else n += ",8w>";
                         }
                         v.push_back(n);
                     }
         return v;
     }();
-    const int di = D == 32 ? 0 : D == 64 ? 1 : D == 128 ? 2 : 3;
-    return names[(((size_t)dtype * 4 + di) * 2 + (general_mod ? 1 : 0)) * 2 + (tile_list ? 1 : 0)].c_str();
+    const int di = D / 32 - 1;
+    return names[(((size_t)dtype * 8 + di) * 2 + (general_mod ? 1 : 0)) * 2 + (tile_list ? 1 : 0)].c_str();
 }
 
 MfmaTiles flash_mfma_tiles(int dtype, int D, bool general_mod, bool tile_list, bool causal) {
     if (dtype == DT_F32) return MfmaTiles{kBlockM32, kBlockNF32 * kTilesF32, kThreads32, false};
     const bool paired = pairs_causal_tiles(causal, tile_list);
     const int bn = block_n16(D, general_mod, tile_list);
-    if (tile_list || D == 256) return MfmaTiles{128, bn, 256, paired};
+    if (tile_list || D > 160) return MfmaTiles{128, bn, 256, paired};
     return MfmaTiles{256, bn, 512, paired};
 }
 

@@ -157,7 +157,8 @@ hipError_t launch_qk_score_mfma(const QkScoreArgs& a, int dtype, hipStream_t s);
 // builds its query tile's list in LDS (no tile_list launch, no workspace).
 size_t list_kernel_lds_bytes(int D, bool lds_list, int num_k_tiles);
 constexpr int kLdsListMaxTiles = 4096;  // key tiles of a list built in LDS
-// Head dims (D == Dv) the MFMA kernels are built for: 32, 64, 128 (fp32) and 256 (bf16/fp16).
+// Head dims (D == Dv) the MFMA kernels are built for: 32, 64, 96, 128 (fp32), every
+// multiple of 32 from 32 to 256 (bf16/fp16).
 bool flash_mfma_head_dim(int dtype, int D);
 const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile_list);
 // Workgroup tiling of the MFMA kernel for a dtype.

@@ -62,7 +62,8 @@ typedef enum ofh_bias_kind {
 } ofh_bias_kind;
 
 /* Which kernel family runs. AUTO picks the MFMA flash kernel when the shape
- * is supported (D == Dv in {32, 64, 128}, or 256 for bf16/fp16; 16-byte aligned rows) and the rowwise
+ * is supported (D == Dv in {32, 64, 96, 128} for fp32, a multiple of 32 up to 256 for bf16/fp16;
+ * 16-byte aligned rows) and the rowwise
  * kernel otherwise. ROWWISE is the exact two-pass softmax of
  * standard_attention, run on the GPU one query row per wavefront. */
 typedef enum ofh_algorithm {

@@ -149,7 +149,7 @@ def test_validation_messages(ofh):
                   "softcap")
     _expect_error(F, F.make_params(1, 1, 4, 4, 64, bias_kind=F.BIAS_ALIBI),
                   F.OFH_ERROR_INVALID_ARGUMENT, "slopes")
-    _expect_error(F, F.make_params(1, 1, 4, 4, 96, algorithm=F.ALGO_FLASH_MFMA),
+    _expect_error(F, F.make_params(1, 1, 4, 4, 80, algorithm=F.ALGO_FLASH_MFMA),
                   F.OFH_ERROR_UNSUPPORTED, "flash MFMA kernel needs")
     _expect_error(F, F.make_params(1, 1, 4, 4, 64, max_key_splits=-1), F.OFH_ERROR_INVALID_ARGUMENT,
                   "max_key_splits")
@@ -177,7 +177,6 @@ def test_kernel_choice(ofh):
         (dict(dtype=F.DTYPE_F16, head_dim=64, mask_allowed=16, mask_query_block_size=64,
               mask_key_block_size=64, mask_query_blocks=4, mask_key_blocks=4),
          "flash_fwd_lockstep_kernel<f16,64,plain,list,4w>"),
-        (dict(dtype=F.DTYPE_BF16, head_dim=96), "rowwise_fwd_kernel"),
         (dict(dtype=F.DTYPE_BF16, head_dim=32), "flash_fwd_lockstep_kernel<bf16,32,plain,8w,128keys>"),
         (dict(dtype=F.DTYPE_F16, head_dim=32, softcap=5.0), "flash_fwd_lockstep_kernel<f16,32,mod,8w,2x64keys>"),
         (dict(dtype=F.DTYPE_BF16, head_dim=256), "flash_fwd_lockstep_kernel<bf16,256,plain,4w>"),
@@ -186,6 +185,11 @@ def test_kernel_choice(ofh):
          "flash_fwd_lockstep_kernel<f16,256,plain,list,4w>"),
         (dict(dtype=F.DTYPE_F32, head_dim=32), "flash_fwd_mfma32_kernel<32,plain>"),
         (dict(dtype=F.DTYPE_F32, head_dim=256), "rowwise_fwd_kernel"),
+        (dict(dtype=F.DTYPE_F32, head_dim=96), "flash_fwd_mfma32_kernel<96,plain>"),
+        (dict(dtype=F.DTYPE_BF16, head_dim=96), "flash_fwd_lockstep_kernel<bf16,96,plain,8w,2x64keys>"),
+        (dict(dtype=F.DTYPE_F16, head_dim=160, softcap=5.0), "flash_fwd_lockstep_kernel<f16,160,mod,8w,2x64keys>"),
+        (dict(dtype=F.DTYPE_BF16, head_dim=192), "flash_fwd_lockstep_kernel<bf16,192,plain,4w>"),
+        (dict(dtype=F.DTYPE_BF16, head_dim=80), "rowwise_fwd_kernel"),
         (dict(dtype=F.DTYPE_BF16, head_dim=64, value_dim=128), "rowwise_fwd_kernel"),
         (dict(dtype=F.DTYPE_F32, head_dim=64, algorithm=F.ALGO_ROWWISE), "rowwise_fwd_kernel"),
     ]

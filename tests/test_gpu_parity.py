@@ -75,7 +75,7 @@ SHAPES = [(1, 1), (7, 13), (64, 64), (128, 128), (200, 333), (333, 200), (1, 204
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
-@pytest.mark.parametrize("D", [32, 64, 128, 256])
+@pytest.mark.parametrize("D", [32, 64, 96, 128, 160, 192, 224, 256])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("splits", [1, 0])
 def test_mfma_shapes(ofh, dt, D, causal, splits):
@@ -577,15 +577,16 @@ def test_rescale_with_score_mod(ofh, dt, splits):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
-@pytest.mark.parametrize("D", [32, 256])
-def test_head_dims_32_and_256(ofh, dt, D):
-    """The MFMA kernels at D = 32 (bf16/fp16/fp32) and D = 256 (bf16/fp16):
-    ALiBi + soft-cap, a dense bias, a block mask (the list kernel), and the
-    lazy rescale with a live accumulator and a negative scale, each with one
+@pytest.mark.parametrize("D", [32, 96, 160, 192, 224, 256])
+def test_head_dims_beyond_64_and_128(ofh, dt, D):
+    """The MFMA kernels at D = 32 and 96 (bf16/fp16/fp32) and 160 ... 256
+    (bf16/fp16; unswizzled rows when D is not a power of two): ALiBi +
+    soft-cap, a dense bias, a block mask (the list kernel), and the lazy
+    rescale with a live accumulator and a negative scale, each with one
     workgroup per query tile and with the key split."""
     F = ofh
-    if dt == "f32" and D == 256:
-        pytest.skip("fp32 runs D = 256 on the rowwise kernel")
+    if dt == "f32" and D > 128:
+        pytest.skip("fp32 runs D > 128 on the rowwise kernel")
     B, H, M, N = 1, 2, 300, 700
     code = {"f32": F.DTYPE_F32, "bf16": F.DTYPE_BF16, "f16": F.DTYPE_F16}[dt]
     assert F.launch_info(F.make_params(B, H, M, N, D, dtype=code)).algorithm == F.ALGO_FLASH_MFMA
