@@ -15,6 +15,7 @@
 #include <mutex>
 #include <string>
 #include <vector>
+#include <vector>
 
 #include "ofh_kernels.h"
 
@@ -139,7 +140,10 @@ void choose_key_splits(const ofh_attention_params* p, Resolved& r) {
     r.split_tiles = 1 << 30;
     if (p->dtype == OFH_DTYPE_F32 && r.paired) return;
     if (p->max_key_splits == 1) return;
-    constexpr int64_t kTarget = 512;
+    // 32-row fp32 blocks: four wavefronts per workgroup, so fewer workgroups
+    // fill the GPU
+    const bool rows32 = p->dtype == OFH_DTYPE_F32 && r.block_m == ofh::kRowsF32;
+    const int64_t kTarget = rows32 ? 256 : 512;
     const int kMaxSplits = p->max_key_splits > 1 ? std::min(p->max_key_splits, 64) : 64;
     const int64_t bh = (int64_t)p->batch * p->heads;
     const int64_t wgs = bh * (r.paired ? (r.num_q_tiles + 1) / 2 : r.num_q_tiles);
@@ -161,7 +165,9 @@ void choose_key_splits(const ofh_attention_params* p, Resolved& r) {
         splits = std::min((max_steps + per - 1) / per, kMaxSplits);
     };
     int splits, per, max_steps;
-    plan(r.block_n, std::max(1, 64 / r.block_n), splits, per, max_steps);  // at least 64 keys per split
+    // at least 64 keys per split (128-row kernels), or a tile per wavefront
+    // (32-row fp32 blocks)
+    plan(r.block_n, rows32 ? 4 : std::max(1, 64 / r.block_n), splits, per, max_steps);
     if (splits <= 1) return;
     r.key_splits = splits;
     r.split_tiles = (max_steps + splits - 1) / splits;
@@ -176,10 +182,11 @@ void set_lds_list(const ofh_attention_params* p, Resolved& r) {
 }
 
 void no_key_split(const ofh_attention_params* p, Resolved& r) {
-    const ofh::MfmaTiles t =
-        ofh::flash_mfma_tiles(p->dtype, (int)p->head_dim, r.general_mod, r.tile_list, p->causal != 0);
     r.key_splits = 1;
     r.split_tiles = 1 << 30;
+    if (p->dtype == OFH_DTYPE_F32 && r.block_m == ofh::kRowsF32) return;  // 32-row blocks: no pairing, no list
+    const ofh::MfmaTiles t =
+        ofh::flash_mfma_tiles(p->dtype, (int)p->head_dim, r.general_mod, r.tile_list, p->causal != 0);
     r.paired = t.paired;
     r.block_n = t.block_n;
     r.num_k_tiles = (int)((p->key_tokens + r.block_n - 1) / r.block_n);
@@ -242,6 +249,16 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
     r.num_q_tiles = (int)((p->query_tokens + r.block_m - 1) / r.block_m);
     r.num_k_tiles = (int)((p->key_tokens + r.block_n - 1) / r.block_n);
     r.tile_list = p->mask_allowed != nullptr;
+    // fp32 with few query tiles (latency-bound): 32-row query blocks whose
+    // four wavefronts share the keys, 32-key tiles
+    if (p->dtype == OFH_DTYPE_F32 && !r.tile_list &&
+        (int64_t)p->batch * p->heads * r.num_q_tiles < ofh::kRows32Below) {
+        r.block_m = ofh::kRowsF32;
+        r.block_n = 32;
+        r.paired = false;
+        r.num_q_tiles = (int)((p->query_tokens + r.block_m - 1) / r.block_m);
+        r.num_k_tiles = (int)((p->key_tokens + r.block_n - 1) / r.block_n);
+    }
     const int64_t grid = (int64_t)p->batch * p->heads * r.num_q_tiles;
     if (grid > std::numeric_limits<int32_t>::max())
         return set_error(OFH_ERROR_UNSUPPORTED, "grid exceeds 2^31 workgroups");
@@ -640,6 +657,19 @@ int ofh_attention_fwd_host(const ofh_attention_params* p, const float* q, const 
     return OFH_SUCCESS;
 }
 
+namespace {
+const char* rows32_kernel_name(int D, bool general) {
+    static const std::vector<std::string> names = [] {
+        std::vector<std::string> v;
+        for (int d = 32; d <= 128; d += 32)
+            for (int gm = 0; gm < 2; ++gm)
+                v.push_back("flash_fwd_f32_rows32_kernel<" + std::to_string(d) + (gm ? ",general>" : ",plain>"));
+        return v;
+    }();
+    return names[(size_t)(D / 32 - 1) * 2 + (general ? 1 : 0)].c_str();
+}
+}  // namespace
+
 int ofh_attention_launch_info(const ofh_attention_params* p, ofh_launch_info* info) {
     if (info == nullptr) return set_error(OFH_ERROR_INVALID_ARGUMENT, "info must be non-null");
     if (int rc = validate(p, false, nullptr, nullptr, nullptr, nullptr)) return rc;
@@ -658,7 +688,9 @@ int ofh_attention_launch_info(const ofh_attention_params* p, ofh_launch_info* in
                            r.key_splits;
         info->key_splits = r.key_splits;
         info->merge_in_launch = merge_in_launch(p, r) ? 1 : 0;
-        name = ofh::flash_mfma_kernel_name(p->dtype, (int)p->head_dim, r.general_mod, r.tile_list);
+        name = (p->dtype == OFH_DTYPE_F32 && r.block_m == ofh::kRowsF32)
+                   ? rows32_kernel_name((int)p->head_dim, r.general_mod)
+                   : ofh::flash_mfma_kernel_name(p->dtype, (int)p->head_dim, r.general_mod, r.tile_list);
     } else {
         info->block_m = 1;
         info->block_n = 64;

@@ -1513,6 +1513,200 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a)
     }
 }
 
+// fp32 calls with few query rows (latency-bound: fewer 128-row query tiles
+// than CUs). A workgroup of four wavefronts covers one 32-row query block and
+// the wavefronts take its 32-key tiles in turn (wavefront w: steps it0 + w,
+// it0 + w + 4, ...), so four times as many wavefronts share the work as in
+// the 128-row kernel. Each keeps its own running (m, l, O) and reads its K and
+// V tiles straight from global memory into the MFMA operand registers (no LDS
+// staging, no barrier in the loop); at the end the four states are folded
+// through LDS with the log-sum-exp rule (attention.cpp:661-674). Key splits
+// across workgroups, and their merge, are those of the 128-row kernel.
+template <int D, bool GENERAL>
+__global__ __launch_bounds__(kThreads32) void flash_fwd_f32_rows32_kernel(FwdArgs a) {
+    constexpr int NO = D / 2;  // O floats per lane
+    constexpr int FS = NO + 2;  // folded floats per lane: O, m, l
+    __shared__ __attribute__((aligned(16))) float fold[3 * FS * 64];
+    static_assert(3 * FS * 64 >= 6 * kThreads32 + 1, "split merge scratch fits in the fold buffer");
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 5, r = lane & 31;
+    int bh, qt;
+    const int tiles_per_split = a.B * a.H * a.num_q_tiles;
+    const int split = (int)blockIdx.x / tiles_per_split;
+    map_work((int)blockIdx.x - split * tiles_per_split, a.B * a.H, a.num_q_tiles, a.causal, bh, qt);
+    const int b = bh / a.H, h = bh - b * a.H;
+    const float* __restrict__ Qp = (const float*)a.q + b * a.q_sb + h * a.q_sh;
+    const float* __restrict__ Kp = (const float*)a.k + b * a.k_sb + h * a.k_sh;
+    const float* __restrict__ Vp = (const float*)a.v + b * a.v_sb + h * a.v_sh;
+    const int q0 = qt * kRowsF32;
+    const int my_q = q0 + r;
+
+    const int kend = a.causal ? min(a.N, q0 + kRowsF32) : a.N;
+    const int ntiles = (kend + kBlockNF32 - 1) / kBlockNF32;
+    const int active = split_active(a, ntiles);
+    if (split >= active) return;  // uniform over the workgroup
+    const int it0 = split * a.split_tiles;
+    const int it1 = min(ntiles, it0 + a.split_tiles);
+
+    // Q^T operand: lane holds Q[my_q][g*D/2 + s] (rows past M: zero)
+    float qf[D / 2];
+    {
+        const float* qrow = Qp + (int64_t)min(my_q, a.M - 1) * a.q_sm + g * (D / 2);
+#pragma unroll
+        for (int c = 0; c < D / 8; ++c) {
+            f32x4 u = *(const f32x4*)(qrow + 4 * c);
+            if (my_q >= a.M) u = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) qf[4 * c + t] = u[t];
+        }
+    }
+    f32x16 o[D / 32];
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) o[db] = f32x16{};
+    float m_run = kNegInf, l_run = 0.0f;
+    const float slope = (GENERAL && a.bias_kind == BIAS_ALIBI) ? a.alibi[h] : 0.0f;
+    const float* bias_row = nullptr;
+    if (GENERAL && a.bias_kind == BIAS_DENSE && my_q < a.M)
+        bias_row = a.bias + b * a.bias_sb + h * a.bias_sh + (int64_t)my_q * a.bias_sm;
+
+    // K/V operand registers of tile it (A operands of S^T = K Q^T and of
+    // O^T += V^T P^T): K[k0 + kappa(r)][g*D/2 + s] and V[k0 + acc_pos(u, g)][r + 32 db].
+    // Rows past N read row N-1 (their scores are masked) and V past N is zero.
+    // Up to D = 64 the next tile of the wavefront is loaded while this one is
+    // computed (registers allow two sets).
+    constexpr bool PREFETCH = D <= 64;
+    struct KV {
+        f32x4 k[D / 8];
+        float v[16][D / 32];
+    };
+    auto load_kv = [&](int it, KV& t) {
+        const int k0 = it * kBlockNF32;
+        const float* krow = Kp + (int64_t)min(k0 + kappa(r), a.N - 1) * a.k_sn + g * (D / 2);
+#pragma unroll
+        for (int c = 0; c < D / 8; ++c) t.k[c] = *(const f32x4*)(krow + 4 * c);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int kj = k0 + acc_pos(u, g);
+            const float* vrow = Vp + (int64_t)min(kj, a.N - 1) * a.v_sn + r;
+#pragma unroll
+            for (int db = 0; db < D / 32; ++db) {
+                const float x = vrow[32 * db];
+                t.v[u][db] = kj < a.N ? x : 0.0f;
+            }
+        }
+    };
+    auto compute = [&](int it, const KV& t) {
+        const int k0 = it * kBlockNF32;
+        f32x16 s[1] = {f32x16{}};
+#pragma unroll
+        for (int c = 0; c < D / 8; ++c)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(t.k[c][j], qf[4 * c + j], s[0], 0, 0, 0);
+        const bool need_mask = (k0 + kBlockNF32 > a.N) || (a.causal && k0 + kBlockNF32 - 1 > q0);
+        const float alpha =
+            online_softmax_tile<1, GENERAL>(a, s, need_mask, my_q, k0, g, slope, bias_row, m_run, l_run);
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) o[db] *= alpha;
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+#pragma unroll
+            for (int db = 0; db < D / 32; ++db)
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(t.v[u][db], s[0][u], o[db], 0, 0, 0);
+    };
+    if constexpr (PREFETCH) {
+        KV cur, nxt;
+        int it = it0 + wave;
+        if (it < it1) load_kv(it, cur);
+        for (; it < it1; it += kWaves32) {
+            const bool more = it + kWaves32 < it1;
+            if (more) load_kv(it + kWaves32, nxt);
+            compute(it, cur);
+            if (more) cur = nxt;
+        }
+    } else {
+        for (int it = it0 + wave; it < it1; it += kWaves32) {
+            KV cur;
+            load_kv(it, cur);
+            compute(it, cur);
+        }
+    }
+
+    // Fold wavefronts 1-3 into wavefront 0 (the four hold the same rows in the
+    // same lane layout); a wavefront that saw no tile has m = -inf, l = 0, O = 0.
+    if (wave > 0) {
+        float* f = fold + (wave - 1) * FS * 64 + lane;
+#pragma unroll
+        for (int i = 0; i < NO; ++i) f[64 * i] = o[i >> 4][i & 15];
+        f[64 * NO] = m_run;
+        f[64 * (NO + 1)] = l_run;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float mg = m_run;
+#pragma unroll
+        for (int w = 0; w < kWaves32 - 1; ++w) mg = fmaxf(mg, fold[w * FS * 64 + 64 * NO + lane]);
+        const float mu = mg == kNegInf ? 0.0f : mg;
+        const float w0 = __builtin_amdgcn_exp2f(m_run - mu);  // 0 while m_run is -inf
+        l_run *= w0;
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) o[db] *= w0;
+#pragma unroll
+        for (int w = 0; w < kWaves32 - 1; ++w) {
+            const float* f = fold + w * FS * 64 + lane;
+            const float ww = __builtin_amdgcn_exp2f(f[64 * NO] - mu);
+            l_run += ww * f[64 * (NO + 1)];
+#pragma unroll
+            for (int i = 0; i < NO; ++i) o[i >> 4][i & 15] += ww * f[64 * i];
+        }
+        m_run = mg;
+    }
+    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    if (active > 1) {
+        // partial row: unnormalised O and (m, l), merged by the last split to arrive
+        const bool coh = a.split_counters != nullptr;
+        if (wave == 0 && my_q < a.M) {
+            const int64_t prow = ((int64_t)split * a.B * a.H + bh) * a.M + my_q;
+            float* po = a.part_o + prow * D + 4 * g;
+#pragma unroll
+            for (int db = 0; db < D / 32; ++db) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    f32x4 val;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) val[j] = o[db][4 * i + j];
+                    put_partial4(po + 32 * db + 8 * i, val, coh);
+                }
+            }
+            if (g == 0) {
+                put_partial(a.part_ml + 2 * prow, m_run, coh);
+                put_partial(a.part_ml + 2 * prow + 1, l_tot, coh);
+            }
+        }
+        if (!coh) return;  // merged by combine_splits_kernel
+        __syncthreads();   // the fold buffer below is reused
+        int* flag = (int*)(fold + 6 * kThreads32);
+        if (split_arrive(a.split_counters + (int64_t)bh * a.num_q_tiles + qt, active, flag))
+            merge_split_rows<float, kThreads32>(a, bh, q0, min(kRowsF32, a.M - q0), active, fold);
+        return;
+    }
+    if (wave == 0 && my_q < a.M) {
+        const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        float* orow = (float*)a.o + b * a.o_sb + h * a.o_sh + (int64_t)my_q * a.o_sm + 4 * g;
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                f32x4 val;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) val[j] = o[db][4 * i + j] * inv;
+                *(f32x4*)(orow + 32 * db + 8 * i) = val;
+            }
+        }
+    }
+}
+
 // Merge of key-split partial rows in a launch of its own (no arrival
 // counters). A workgroup merges `rows` consecutive rows of one head (a power
 // of two, so they lie in one query tile): thread t takes (row, 4-column chunk)
@@ -1666,6 +1860,20 @@ hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipS
             default: return hipErrorInvalidValue;
         }
     } else if (dtype == DT_F32) {
+        if (a.split_bm == kRowsF32) {  // few query rows: 32-row blocks (no block mask)
+            if (a.tile_counts != nullptr) return hipErrorInvalidValue;
+            switch (a.D) {
+                case 32: return general_mod ? launch(flash_fwd_f32_rows32_kernel<32, true>, kThreads32, a, s)
+                                            : launch(flash_fwd_f32_rows32_kernel<32, false>, kThreads32, a, s);
+                case 64: return general_mod ? launch(flash_fwd_f32_rows32_kernel<64, true>, kThreads32, a, s)
+                                            : launch(flash_fwd_f32_rows32_kernel<64, false>, kThreads32, a, s);
+                case 96: return general_mod ? launch(flash_fwd_f32_rows32_kernel<96, true>, kThreads32, a, s)
+                                            : launch(flash_fwd_f32_rows32_kernel<96, false>, kThreads32, a, s);
+                case 128: return general_mod ? launch(flash_fwd_f32_rows32_kernel<128, true>, kThreads32, a, s)
+                                             : launch(flash_fwd_f32_rows32_kernel<128, false>, kThreads32, a, s);
+                default: return hipErrorInvalidValue;
+            }
+        }
         if (a.D == 96)
             return general_mod ? launch(flash_fwd_mfma32_kernel<96, true, kTilesF32>, kThreads32, a, s)
                                : launch(flash_fwd_mfma32_kernel<96, false, kTilesF32>, kThreads32, a, s);

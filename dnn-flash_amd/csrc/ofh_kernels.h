@@ -14,6 +14,11 @@ enum Bias : int { BIAS_NONE = 0, BIAS_ALIBI = 1, BIAS_DENSE = 2 };
 // MFMA column block); the workgroup shape depends on the element type.
 constexpr int kQueriesPerWave = 32;
 
+// fp32 calls with fewer 128-row query tiles than this run 32-row query
+// blocks, four wavefronts per block sharing its keys (flash_fwd_f32_rows32_kernel).
+constexpr int kRowsF32 = 32;
+constexpr int kRows32Below = 128;
+
 struct MfmaTiles {
     int block_m;  // query rows per query tile
     int block_n;  // keys per K/V tile

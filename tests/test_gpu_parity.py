@@ -88,6 +88,30 @@ def test_mfma_shapes(ofh, dt, D, causal, splits):
         check(out, ref, dt, f"{dt} D{D} causal={causal} M{M} N{N} max_key_splits={splits}")
 
 
+@pytest.mark.parametrize("D", [32, 64, 96, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_f32_row_blocks(ofh, D, causal):
+    """fp32 calls with fewer than 128 query tiles of 128 rows run 32-row query
+    blocks (four wavefronts share each block's keys and fold their states in
+    LDS); larger calls run the 128-row kernel. Both against the oracle, with
+    and without the key split (in-launch merge), plain and ALiBi + soft-cap."""
+    F = ofh
+    for B, H, M, N, kind in [(1, 2, 200, 333, "rows32"), (8, 16, 200, 333, "mfma32")]:
+        p = F.make_params(B, H, M, N, D, dtype=F.DTYPE_F32, causal=causal)
+        name = F.launch_info(p).kernel_name.decode()
+        assert kind in name, name
+        dev, host = make_inputs("f32", B, H, M, N, D, seed=D + causal)
+        for splits in (1, 0):
+            out = run(ofh, dev, dt="f32", causal=causal, max_key_splits=splits)
+            check(out, oracle_full(host, causal=causal), "f32",
+                  f"{name} B{B} H{H} M{M} N{N} causal={causal} max_key_splits={splits}")
+        if kind == "rows32":
+            slopes = alibi_slopes(H)
+            out = run(ofh, dev, dt="f32", causal=causal, slopes=slopes, softcap=5.0)
+            check(out, oracle_full(host, causal=causal, slopes=slopes, softcap=5.0), "f32",
+                  f"{name} ALiBi + soft-cap 5 causal={causal}")
+
+
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
 def test_score_mods(ofh, dt):
     B, H, M, N, D = 2, 4, 190, 257, 128 if dt != "f16" else 64
