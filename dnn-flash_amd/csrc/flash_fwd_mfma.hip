@@ -466,10 +466,9 @@ __device__ __forceinline__ void dma16(const void* g, unsigned lds) {
 // are transposing reads of 4 rows x 2 chunks per 16 lanes. For D = 64 two rows
 // share a 256-byte bank line, hence row >> 1.
 //
-// Head dims that are not powers of two (96, 160, 192, 224) keep rows
-// unswizzled: chunk c of row r at position c, read at offset + 32c (K) and
-// + 64 db (V) instead of an XOR (their rows are not a power-of-two number of
-// chunks, so an XOR could leave the row).
+// Head dims that are not powers of two (96, 160, 192, 224) XOR only inside
+// aligned groups of chunks that divide the row (see kswz), and their reads add
+// per-lane bases to compile-time offsets instead of XORing the address.
 template <int D, int BN>
 struct TileLayout {
     static constexpr int RB = D * 2;              // bytes of one K/V row
@@ -482,15 +481,27 @@ struct TileLayout {
     // copies (8 rows with 4 wavefronts at D = 256). The V swizzle must also
     // repeat every 4 rows: a V^T fragment is two transposing reads 4 rows
     // apart at one lane offset.
+    //
+    // Rows that are not a power of two wide (D = 96, 160, 192, 224): a
+    // 16-byte K read serves 16 lanes at a time, rows kappa(0..15) at one
+    // chunk, and with 12, 20 or 28 chunks per row those rows start on only 4
+    // distinct 16-byte bank groups (2 at 24 chunks). The chunk index is XORed
+    // inside aligned groups of KG chunks (KG divides the row): by (row>>2)&3
+    // (KG = 4), so the 16 rows cover the 16 bank groups, or by (row>>1)&7 at
+    // D = 192 (KG = 8). A V^T read serves rows 4 apart in 64-byte runs, which
+    // already fall on distinct banks except at D = 192 (rows 384 bytes apart):
+    // there chunks are XORed with 4 on (row>>1)&1.
+    static constexpr int KG = POW2 ? 1 : (D == 192 ? 8 : 4);
+    static_assert(POW2 || CPR % KG == 0, "the K swizzle group divides the row");
     static __device__ __forceinline__ int kswz(int row) {
-        if (!POW2) return 0;
+        if (!POW2) return D == 192 ? (row >> 1) & 7 : (row >> 2) & 3;
         if (D == 256) return row & 7;
         if (D == 128) return row & 15;
         if (D == 64) return (row >> 1) & 7;
         return (row >> 2) & 3;  // D = 32: four rows share a bank line
     }
     static __device__ __forceinline__ int vswz(int row) {
-        if (!POW2) return 0;
+        if (!POW2) return D == 192 ? 4 * ((row >> 1) & 1) : 0;
         if (D >= 128) return 4 * (row & 3);
         if (D == 64) return 4 * ((row >> 1) & 1);
         return 0;  // D = 32: a row is one 32-column block
@@ -563,6 +574,11 @@ struct Wave32 {
     const float* bias_row;
     // LDS read lane offsets
     int k_lane_off, v_lane_off;
+    // rows that are not a power of two wide: per-lane bases of the swizzled
+    // chunk pairs (K) and 32-column blocks (V at D = 192), the rest of the
+    // offset is a compile-time immediate
+    int k_base[L::POW2 ? 1 : L::KG / 2];
+    int v_base[L::POW2 ? 1 : 2];
     // K/V copies: lane offsets (elements) of its chunk in rows dma_row0 + u*DSTEP
     // when a copy instruction covers whole rows (64 * wavefronts divisible by
     // the chunks per row: every power-of-two D); otherwise each instruction's
@@ -572,11 +588,20 @@ struct Wave32 {
     static_assert(!UNIFORM_COPY || !L::POW2 ||
                       DSTEP % (D == 256 ? 8 : D == 128 ? 16 : D == 64 ? 32 : 64) == 0,
                   "the K/V swizzles must repeat within the rows one copy lane covers");
-    static_assert(UNIFORM_COPY || !L::POW2, "unswizzled rows when an instruction splits a row");
+    static_assert(UNIFORM_COPY || !L::POW2, "power-of-two rows are copied by whole-row instructions");
+    static_assert(L::POW2 || !UNIFORM_COPY, "rows that are not a power of two wide are copied slot by slot");
     int dma_row0, dma_koff, dma_voff;
     // K fragment c (chunks 2c, 2c+1) and V^T block db at the lane's read offsets
-    __device__ __forceinline__ int k_off(int c) const { return L::POW2 ? (k_lane_off ^ (32 * c)) : k_lane_off + 32 * c; }
-    __device__ __forceinline__ int v_off(int db) const { return L::POW2 ? (v_lane_off ^ (64 * db)) : v_lane_off + 64 * db; }
+    __device__ __forceinline__ int k_off(int c) const {
+        if constexpr (L::POW2) return k_lane_off ^ (32 * c);
+        // chunk (2c + g) ^ s = (2c & ~(KG-1)) + ((2c & (KG-1)) ^ (g ^ s))
+        else return k_base[c % (L::KG / 2)] + 16 * ((2 * c) & ~(L::KG - 1));
+    }
+    __device__ __forceinline__ int v_off(int db) const {
+        if constexpr (L::POW2) return v_lane_off ^ (64 * db);
+        else if constexpr (D == 192) return v_base[db & 1] + 64 * (db & ~1);
+        else return v_lane_off + 64 * db;
+    }
 
     __device__ __forceinline__ Wave32(const FwdArgs& args, unsigned char* sm, int bh, int q0, int wv)
         : a(args), smem(sm), wave(wv) {
@@ -616,9 +641,18 @@ struct Wave32 {
         // K chunk 2c+g of row kappa(r) sits at 32 (c ^ kh) + 16 gl: read at k_lane_off ^ 32c
         const int ksw = L::kswz(kappa(r));
         k_lane_off = kappa(r) * L::KSTR + 16 * ((g ^ ksw) & 1) + 32 * (ksw >> 1);
+        if constexpr (!L::POW2) {
+#pragma unroll
+            for (int jj = 0; jj < L::KG / 2; ++jj) k_base[jj] = kappa(r) * L::KSTR + 16 * ((2 * jj) ^ (g ^ ksw));
+        }
         // V chunk (v_dquad>>3) + 4 db of row 8g + j/4 sits at chunk + 4 (db ^ rq): read at v_lane_off ^ 64 db
         const int rq = L::vswz(8 * g + (j >> 2)) >> 2;
         v_lane_off = L::KTILE + (8 * g + (j >> 2)) * L::VSTR + (v_dquad >> 3) * 16 + (v_dquad & 4) * 2 + 64 * rq;
+        if constexpr (!L::POW2) {
+            const int vb0 = L::KTILE + (8 * g + (j >> 2)) * L::VSTR + (v_dquad >> 3) * 16 + (v_dquad & 4) * 2;
+            v_base[0] = vb0 + 64 * rq;
+            v_base[1] = vb0 + 64 * (1 ^ rq);
+        }
         // copies: wave instruction u covers 16-byte slots 64 (u NWAVES + wave) + lane
         const int slot0 = 64 * wave + lane;
         dma_row0 = slot0 / L::CPR;
@@ -648,14 +682,14 @@ struct Wave32 {
         const unsigned lds0 = (unsigned)(uintptr_t)smem + stage_off + 1024 * wave;
         constexpr int NW = NTHREADS / 64;
         if constexpr (!UNIFORM_COPY) {
-            // slot 64 (u NW + wave) + lane: row slot / CPR, chunk slot % CPR (unswizzled)
+            // slot 64 (u NW + wave) + lane: row slot / CPR, position slot % CPR
 #pragma unroll
             for (int u = 0; u < CPT; ++u) {
                 const int slot = 64 * (u * NW + wave) + (tid & 63);
                 const int row = slot / L::CPR, pos = slot - row * L::CPR;
                 const int rr = min(k0 + row, a.N - 1) - k0;
-                dma16(kt_base + (int64_t)rr * a.k_sn + 8 * pos, lds0 + 1024 * NW * u);
-                dma16(vt_base + (int64_t)rr * a.v_sn + 8 * pos, lds0 + L::KTILE + 1024 * NW * u);
+                dma16(kt_base + (int64_t)rr * a.k_sn + 8 * (pos ^ L::kswz(row)), lds0 + 1024 * NW * u);
+                dma16(vt_base + (int64_t)rr * a.v_sn + 8 * (pos ^ L::vswz(row)), lds0 + L::KTILE + 1024 * NW * u);
             }
             return;
         }
