@@ -1927,11 +1927,13 @@ hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipS
 hipError_t launch_combine_splits(const FwdArgs& a, int dtype, hipStream_t s) {
     const int chunks = a.Dv / 4;
     if (a.B * a.H * a.M <= 0 || chunks <= 0 || chunks > 256 || a.split_bm <= 0) return hipErrorInvalidValue;
-    // splits per row read in parallel: up to 8 groups (two rounds of four
-    // loads per thread for 64 splits); rows per workgroup: a power of two
-    // dividing the query tile, with rows * chunks * groups <= 256
+    // splits per row read in parallel: a thread keeps four splits' loads in
+    // flight, so a group is added only while each would read more than four
+    // (up to 8 groups: two rounds of four loads per thread for 64 splits);
+    // rows per workgroup: a power of two dividing the query tile, with
+    // rows * chunks * groups <= 256
     int groups = 1;
-    while (groups < 8 && groups < a.num_splits && 2 * groups * chunks <= 256) groups *= 2;
+    while (groups < 8 && 4 * groups < a.num_splits && 2 * groups * chunks <= 256) groups *= 2;
     int rows = 1;
     while (2 * rows * chunks * groups <= 256 && 2 * rows <= a.split_bm && a.split_bm % (2 * rows) == 0) rows *= 2;
     const int64_t nblk = (int64_t)a.B * a.H * ((a.M + rows - 1) / rows);
