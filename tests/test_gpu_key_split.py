@@ -180,16 +180,18 @@ def test_max_key_splits(ofh):
         check(out, ref, "bf16", f"max_key_splits={cap} (splits {ks})")
 
 
-def test_graph_capture(ofh):
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_graph_capture(ofh, dt):
     """A split call captured in a HIP graph: with a caller workspace the split
     (and its in-launch merge) is kept; without one, on the capture stream whose
-    library buffer is empty, the split is dropped rather than allocating. Every
-    replay, with eager calls in between, gives the oracle's rows."""
+    library buffer is empty, the split is dropped rather than allocating (fp32:
+    the 32-row query blocks stay). Every replay, with eager calls in between,
+    gives the oracle's rows."""
     F = ofh
     B, H, M, N, D = 1, 4, 2, 8192, 128
-    dev, host = make_inputs("bf16", B, H, M, N, D, seed=31)
+    dev, host = make_inputs(dt, B, H, M, N, D, seed=31)
     ref = oracle_rows(host, False, 1.0 / math.sqrt(D))
-    p = F.make_params(B, H, M, N, D, dtype=DTYPE["bf16"], out_dtype=DTYPE["f32"])
+    p = F.make_params(B, H, M, N, D, dtype=DTYPE[dt], out_dtype=DTYPE["f32"])
     info = F.launch_info(p)
     assert info.key_splits > 1 and info.merge_in_launch == 1
     ws = torch.empty(F.workspace_bytes(p), dtype=torch.uint8, device="cuda")
@@ -203,7 +205,7 @@ def test_graph_capture(ofh):
             out.fill_(float("nan"))
             g.replay()
             torch.cuda.synchronize()
-            check(out.cpu().numpy(), ref, "bf16", f"graph replay {rep} workspace={use_ws}")
+            check(out.cpu().numpy(), ref, dt, f"{dt} graph replay {rep} workspace={use_ws}")
             eager = F.attention_fwd(*dev, scale=scale, out_dtype=torch.float32)
             torch.cuda.synchronize()
-            check(eager.cpu().numpy(), ref, "bf16", f"eager call after replay {rep}")
+            check(eager.cpu().numpy(), ref, dt, f"{dt} eager call after replay {rep}")
