@@ -143,7 +143,10 @@ void choose_key_splits(const ofh_attention_params* p, Resolved& r) {
     // 32-row fp32 blocks: four wavefronts per workgroup, so fewer workgroups
     // fill the GPU
     const bool rows32 = p->dtype == OFH_DTYPE_F32 && r.block_m == ofh::kRowsF32;
-    const int64_t kTarget = rows32 ? 256 : 512;
+    // 128-row fp32 tiles run two workgroups per CU and a split step is long:
+    // about 384 workgroups (fp32 causal B2 H8 N2048: 3 splits, 126 us, against
+    // 135 us with 4 and 171 us with 2)
+    const int64_t kTarget = rows32 ? 256 : (p->dtype == OFH_DTYPE_F32 ? 384 : 512);
     const int kMaxSplits = p->max_key_splits > 1 ? std::min(p->max_key_splits, 64) : 64;
     const int64_t bh = (int64_t)p->batch * p->heads;
     const int64_t wgs = bh * (r.paired ? (r.num_q_tiles + 1) / 2 : r.num_q_tiles);
