@@ -135,45 +135,70 @@ int validate(const ofh_attention_params* p, bool check_ptrs, const void* q, cons
 // calls then run their query tiles unpaired. Without a mask the tile steps of
 // query tile qt are known on the host; with a block mask the list can only
 // remove steps, so the unmasked count is an upper bound.
+// Workgroups that run at once per CU for the kernel the call takes (registers
+// and LDS of the kernels in flash_fwd_mfma.hip): the 8-wavefront 16-bit
+// kernels one, the 4-wavefront ones two up to D = 128, the fp32 kernels two up
+// to D = 64.
+int workgroups_per_cu(const ofh_attention_params* p, const Resolved& r) {
+    if (p->dtype == OFH_DTYPE_F32) return p->head_dim <= 64 ? 2 : 1;
+    if (r.threads >= 512) return 1;
+    return p->head_dim < 160 ? 2 : 1;
+}
+constexpr int64_t kComputeUnits = 256;  // MI355X
+
+// Key split for calls with fewer query tiles than the GPU runs at once: every
+// query tile's K/V tile steps are cut into ranges of `per` steps, one
+// workgroup each. The split count is the largest whose workgroups (those with
+// steps to run) all fit in one round of the GPU's slots (CUs x workgroups per
+// CU): a second round doubles the longest chain, and every extra split adds
+// partial rows to store and merge. Measured (per call): bf16 decode B1 H8 M1
+// N32768 D128 30.9 us with 32 splits against 36.0 with 64; bf16 causal B1 H8
+// N4096 D128 61.3 us with 3 against 87.7 with 7; fp32 causal B2 H8 N2048 D64
+// 126 us with 3 against 135 with 4.
 void choose_key_splits(const ofh_attention_params* p, Resolved& r) {
     r.key_splits = 1;
     r.split_tiles = 1 << 30;
     if (p->dtype == OFH_DTYPE_F32 && r.paired) return;
     if (p->max_key_splits == 1) return;
-    // 32-row fp32 blocks: four wavefronts per workgroup, so fewer workgroups
-    // fill the GPU
     const bool rows32 = p->dtype == OFH_DTYPE_F32 && r.block_m == ofh::kRowsF32;
-    // 128-row fp32 tiles run two workgroups per CU and a split step is long:
-    // about 384 workgroups (fp32 causal B2 H8 N2048: 3 splits, 126 us, against
-    // 135 us with 4 and 171 us with 2)
-    const int64_t kTarget = rows32 ? 256 : (p->dtype == OFH_DTYPE_F32 ? 384 : 512);
+    const int64_t slots = kComputeUnits * workgroups_per_cu(p, r);
     const int kMaxSplits = p->max_key_splits > 1 ? std::min(p->max_key_splits, 64) : 64;
     const int64_t bh = (int64_t)p->batch * p->heads;
     const int64_t wgs = bh * (r.paired ? (r.num_q_tiles + 1) / 2 : r.num_q_tiles);
-    if (wgs >= kTarget) return;
-    // splits and steps per split for K/V tiles of block_n keys, each split
-    // at least min_steps tile steps
-    auto plan = [&](int block_n, int min_steps, int& splits, int& per, int& max_steps) {
-        int64_t total = 0;
-        max_steps = 0;
-        for (int qt = 0; qt < r.num_q_tiles; ++qt) {
-            const int64_t kend = p->causal ? std::min<int64_t>((int64_t)p->key_tokens, (int64_t)(qt + 1) * r.block_m)
-                                           : (int64_t)p->key_tokens;
-            const int steps = (int)((kend + block_n - 1) / block_n);
-            total += steps;
-            max_steps = std::max(max_steps, steps);
-        }
-        total *= bh;
-        per = (int)std::max<int64_t>(min_steps, (total + kTarget - 1) / kTarget);
-        splits = std::min((max_steps + per - 1) / per, kMaxSplits);
+    if (wgs >= slots) return;
+    // tile steps of each query tile (block_n keys each)
+    std::vector<int> steps((size_t)r.num_q_tiles);
+    int max_steps = 0;
+    for (int qt = 0; qt < r.num_q_tiles; ++qt) {
+        const int64_t kend = p->causal ? std::min<int64_t>((int64_t)p->key_tokens, (int64_t)(qt + 1) * r.block_m)
+                                       : (int64_t)p->key_tokens;
+        steps[(size_t)qt] = (int)((kend + r.block_n - 1) / r.block_n);
+        max_steps = std::max(max_steps, steps[(size_t)qt]);
+    }
+    // at least 64 keys per split (128/256-row kernels), or a tile per
+    // wavefront (32-row fp32 blocks)
+    const int min_steps = rows32 ? 4 : std::max(1, 64 / r.block_n);
+    const int most = std::min(kMaxSplits, std::max(1, max_steps / min_steps));
+    auto per_of = [&](int n) { return (max_steps + n - 1) / n; };
+    auto active = [&](int n) {
+        const int per = per_of(n);
+        int64_t a = 0;
+        for (int st : steps) a += (st + per - 1) / per;
+        return a * bh;
     };
-    int splits, per, max_steps;
-    // at least 64 keys per split (128-row kernels), or a tile per wavefront
-    // (32-row fp32 blocks)
-    plan(r.block_n, rows32 ? 4 : std::max(1, 64 / r.block_n), splits, per, max_steps);
+    // largest split count in [1, most] whose active workgroups fit the slots
+    // (active grows with the count)
+    int lo = 1, hi = most;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) / 2;
+        if (active(mid) <= slots) lo = mid;
+        else hi = mid - 1;
+    }
+    const int per = per_of(lo);
+    const int splits = (max_steps + per - 1) / per;
     if (splits <= 1) return;
     r.key_splits = splits;
-    r.split_tiles = (max_steps + splits - 1) / splits;
+    r.split_tiles = per;
     r.paired = false;
 }
 

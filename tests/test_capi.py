@@ -209,16 +209,18 @@ def test_kernel_choice(ofh):
     assert info.workgroups == 4 * 32 * 8 and info.block_m == 256 and info.threads == 512
     assert info.key_splits == 1
     # 16-bit decode: 8 heads x 1 query tile -> 256 staged 128-key tiles per head
-    # in 64 splits of 4 (512 workgroups)
+    # in 32 splits of 8: 256 workgroups, one round of the 256 CUs (one
+    # 8-wavefront workgroup per CU)
     info = F.launch_info(F.make_params(1, 8, 1, 32768, 128, dtype=F.DTYPE_BF16))
-    assert info.key_splits == 64 and info.workgroups == 8 * 64
+    assert info.key_splits == 32 and info.workgroups == 8 * 32
     assert F.launch_info(F.make_params(1, 8, 1, 32768, 128, dtype=F.DTYPE_BF16,
                                        max_key_splits=1)).key_splits == 1
     assert F.launch_info(F.make_params(1, 8, 1, 32768, 128, dtype=F.DTYPE_BF16,
                                        max_key_splits=3)).key_splits == 3
-    # causal with too few pairs: unpaired query tiles (16 per head), split
+    # causal with too few pairs: unpaired query tiles (16 per head, 2..32 staged
+    # tiles), 3 splits of 11: 256 workgroups with steps to run
     info = F.launch_info(F.make_params(1, 8, 4096, 4096, 128, dtype=F.DTYPE_BF16, causal=True))
-    assert info.key_splits == 7 and info.workgroups == 8 * 16 * 7
+    assert info.key_splits == 3 and info.workgroups == 8 * 16 * 3
     info = F.launch_info(F.make_params(4, 32, 4096, 4096, 128, dtype=F.DTYPE_BF16))
     assert info.workgroups == 4 * 32 * 16
     assert info.key_splits == 1 and info.block_n == 128   # staged keys per barrier (2 x 64 computed)
