@@ -10,6 +10,7 @@
 #include <cstring>
 #include <stdexcept>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "onednn_flash/attention.hpp"
@@ -189,8 +190,36 @@ std::vector<float> run_vectors(const std::vector<float>& q, const std::vector<fl
 // ---------------------------------------------------------------------------
 // AttentionWorkspace
 
+namespace {
+// the host tile buffers, member by member (copy or move)
+template <typename Src>
+void assign_host_tiles(AttentionWorkspace& d, Src&& s) {
+    d.q_tile = std::forward<Src>(s).q_tile;
+    d.k_tile_t = std::forward<Src>(s).k_tile_t;
+    d.v_tile = std::forward<Src>(s).v_tile;
+    d.score_tile = std::forward<Src>(s).score_tile;
+    d.p_tile = std::forward<Src>(s).p_tile;
+    d.pv_tile = std::forward<Src>(s).pv_tile;
+    d.running_max = std::forward<Src>(s).running_max;
+    d.running_sum = std::forward<Src>(s).running_sum;
+    d.acc = std::forward<Src>(s).acc;
+    d.old_scales = std::forward<Src>(s).old_scales;
+    d.new_maxes = std::forward<Src>(s).new_maxes;
+    d.block_sums = std::forward<Src>(s).block_sums;
+    d.row_has_valid = std::forward<Src>(s).row_has_valid;
+}
+}  // namespace
+
+AttentionWorkspace::AttentionWorkspace(const AttentionWorkspace& other) { assign_host_tiles(*this, other); }
+
+AttentionWorkspace& AttentionWorkspace::operator=(const AttentionWorkspace& other) {
+    if (this != &other) assign_host_tiles(*this, other);  // the device staging area stays this workspace's own
+    return *this;
+}
+
 AttentionWorkspace::AttentionWorkspace(AttentionWorkspace&& other) noexcept
     : device_buffer(other.device_buffer), device_bytes(other.device_bytes), device(other.device) {
+    assign_host_tiles(*this, std::move(other));
     other.device_buffer = nullptr;
     other.device_bytes = 0;
     other.device = -1;
@@ -199,6 +228,7 @@ AttentionWorkspace::AttentionWorkspace(AttentionWorkspace&& other) noexcept
 AttentionWorkspace& AttentionWorkspace::operator=(AttentionWorkspace&& other) noexcept {
     if (this != &other) {
         if (device_buffer != nullptr) (void)hipFree(device_buffer);
+        assign_host_tiles(*this, std::move(other));
         device_buffer = other.device_buffer;
         device_bytes = other.device_bytes;
         device = other.device;
@@ -215,6 +245,15 @@ AttentionWorkspace::~AttentionWorkspace() {
 
 void AttentionWorkspace::resize(std::size_t q_block_size, std::size_t k_block_size,
                                 std::size_t head_dim, std::size_t value_dim) {
+    q_tile.resize(q_block_size * head_dim);
+    k_tile_t.resize(head_dim * k_block_size);
+    v_tile.resize(k_block_size * value_dim);
+    score_tile.resize(q_block_size * k_block_size);
+    p_tile.resize(q_block_size * k_block_size);
+    pv_tile.resize(q_block_size * value_dim);
+    for (auto* row : {&running_max, &running_sum, &old_scales, &new_maxes, &block_sums}) row->resize(q_block_size);
+    acc.resize(q_block_size * value_dim);
+    row_has_valid.resize(q_block_size);
     reserve_device_bytes(4 * (q_block_size * head_dim + k_block_size * (head_dim + value_dim) +
                               q_block_size * value_dim));
 }

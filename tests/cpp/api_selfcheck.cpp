@@ -13,6 +13,7 @@
 #include <cstring>
 #include <stdexcept>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "onednn_flash/attention.hpp"
@@ -176,6 +177,23 @@ int main() {
     void* const first_buffer = ws.device_buffer;
     of::flash_attention_qk_pv_tile_ws(q.data(), k.data(), v.data(), out_ws.data(), shape, tile_opts, ws);
     expect(ws.device_buffer == first_buffer, "workspace reused without reallocation", 0.0);
+    {
+        // the reference's public tile buffers, sized by resize() as there
+        of::AttentionWorkspace w2;
+        w2.resize(32, 64, 16, 8);
+        const bool sizes = w2.q_tile.size() == 32 * 16 && w2.k_tile_t.size() == 16 * 64 && w2.v_tile.size() == 64 * 8 &&
+                           w2.score_tile.size() == 32 * 64 && w2.p_tile.size() == 32 * 64 &&
+                           w2.pv_tile.size() == 32 * 8 && w2.acc.size() == 32 * 8 && w2.running_max.size() == 32 &&
+                           w2.running_sum.size() == 32 && w2.old_scales.size() == 32 && w2.new_maxes.size() == 32 &&
+                           w2.block_sums.size() == 32 && w2.row_has_valid.size() == 32;
+        w2.q_tile[5] = 3.0f;
+        of::AttentionWorkspace w3 = w2;  // copy: host buffers, no shared device memory
+        const bool copied = w3.q_tile.size() == w2.q_tile.size() && w3.q_tile[5] == 3.0f &&
+                            w3.device_buffer == nullptr && w2.device_buffer != nullptr;
+        of::AttentionWorkspace w4 = std::move(w2);  // move: both, and the source gives up its device memory
+        const bool moved = w4.q_tile.size() == 32 * 16 && w4.device_buffer != nullptr && w2.device_buffer == nullptr;
+        expect(sizes && copied && moved, "workspace tile buffers, copy and move", sizes + 2.0 * copied + 4.0 * moved);
+    }
     expect(of::max_abs_diff(standard, out_ws) <= 1e-5f, "flash_attention_qk_pv_tile_ws vs standard",
            of::max_abs_diff(standard, out_ws));
 
