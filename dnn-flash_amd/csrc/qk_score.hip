@@ -279,6 +279,171 @@ __global__ __launch_bounds__(256) void qk_score_mfma_kernel(QkScoreArgs a) {
     }
 }
 
+// Score rows without a bias or soft-cap, K <= 128 (scores only need the scale):
+// one workgroup per 128-row query block and run of `tpw` 128-key blocks.
+// The query block's MFMA fragments stay in registers for the whole run; K
+// block t+1 is copied global -> LDS into the second buffer while block t is
+// multiplied and written, and the buffer block t was read from then stages
+// its epilogue (the same 256-byte row segments as above). 64 KB of LDS, two
+// workgroups per CU. A one-block workgroup serialises its copies, MFMAs and
+// stores (0.59-0.65 ms for 32 heads x 4096^2 x 128, against 0.35 ms for the
+// stores alone); streaming K blocks through two buffers overlaps them.
+// Workgroups are numbered so that each XCD (workgroup n runs on XCD n mod 8)
+// takes a contiguous range of query blocks, i.e. reads the Q and K of a few
+// heads only. Same products and summation order as qk_score_mfma_kernel, so
+// the scores are bit-identical. CH = 16-byte chunks per K row in LDS (K <= 8 CH).
+constexpr int kRowBufBytes = 32 * 1024;   // one K block (128 rows x 16 CH bytes), or the epilogue staging
+
+template <int CH>
+__device__ __forceinline__ int row_swz(int row) {
+    // chunk position XOR: 16 consecutive rows of a fragment read hit 16 distinct 16-byte bank groups
+    return CH == 16 ? (row & 15) : CH == 8 ? ((row >> 1) & 7) : ((row >> 2) & 3);
+}
+
+template <typename T, int CH>
+__global__ __launch_bounds__(256, 2) void qk_score_mfma_rows_kernel(QkScoreArgs a, int64_t nqb, int64_t npieces,
+                                                                    int tpw) {
+#pragma clang fp contract(off)
+    __shared__ __attribute__((aligned(16))) unsigned char smem[2 * kRowBufBytes];
+    constexpr int RB = CH * 16;    // LDS bytes per K row
+    constexpr int RPI = 64 / CH;   // K rows per wavefront copy instruction (1 KB of LDS)
+    constexpr int STEPS = CH / 2;  // 16-wide k steps
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 31, half = lane >> 5;
+    const int64_t total = gridDim.x, n = blockIdx.x, per = total / 8;
+    const int64_t id = n < 8 * per ? (n % 8) * per + n / 8 : n;
+    const int64_t piece = id % npieces;
+    const int64_t qb = (id / npieces) % nqb;
+    const int64_t bt = id / (npieces * nqb);
+    const int64_t nkb = (a.N + kMfmaBlock - 1) / kMfmaBlock;
+    const int64_t kb_begin = piece * tpw;
+    const int64_t kb_end = min(nkb, kb_begin + tpw);
+    const T* q = (const T*)a.q + bt * a.a_sb;
+    const T* k = (const T*)a.k + bt * a.b_sb;
+    qk_lds_u8* lds = (qk_lds_u8*)smem;
+    const qk_u32x4 zero = {0u, 0u, 0u, 0u};
+    const int64_t i0 = qb * kMfmaBlock + (wave >> 1) * 64;   // the wavefront's 64 query rows
+    // B-operand fragments of the wavefront's query rows (rows past M clamped, chunks past K zero)
+    qk_u32x4 qf[2][STEPS];
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+        const int64_t qr = min(i0 + 32 * x + r, a.M - 1);
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st) {
+            const int c = 2 * st + half;
+            qf[x][st] = 8 * c < a.K ? *(const qk_u32x4*)(q + qr * a.a_sm + 8 * c) : zero;
+        }
+    }
+    // K block kb -> LDS buffer buf: wavefront w, step u copies rows (4u + w) RPI .. +RPI-1; lane L
+    // writes row (4u + w) RPI + L / CH, position L % CH, holding global chunk (L % CH) ^ row_swz(row).
+    // Rows past N and chunks past K read clamped in-range addresses; their values are never used.
+    // Lane offsets are 32-bit from the block's base (the launcher checks 128 b_sn fits).
+    const int bsn = (int)a.b_sn;
+    auto copy_k = [&](int64_t kb, int buf) {
+        const T* kblk = k + kb * kMfmaBlock * a.b_sn;
+        const int lim = (int)min((int64_t)kMfmaBlock - 1, a.N - 1 - kb * kMfmaBlock);
+#pragma unroll
+        for (int u = 0; u < CH / 2; ++u) {
+            const int slot = 4 * u + wave;
+            const int row = slot * RPI + lane / CH;
+            const int c = (lane % CH) ^ row_swz<CH>(row);
+            const int kc = 8 * c < a.K ? 8 * c : 0;
+            dma16(kblk + (min(row, lim) * bsn + kc), lds + buf * kRowBufBytes + slot * 1024);
+        }
+    };
+    int koff[2], ksw[2];
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+        const int kr = (wave & 1) * 64 + 32 * y + r;
+        koff[y] = kr * RB;
+        ksw[y] = row_swz<CH>(kr);
+    }
+    copy_k(kb_begin, 0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the first K block and the Q fragments
+    __syncthreads();
+    for (int64_t kb = kb_begin; kb < kb_end; ++kb) {
+        const int buf = (int)((kb - kb_begin) & 1);
+        if (kb + 1 < kb_end) copy_k(kb + 1, buf ^ 1);
+        qk_lds_u8* kl = lds + buf * kRowBufBytes;
+        qk_f32x16 acc[2][2];
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+            for (int y = 0; y < 2; ++y)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[x][y][e] = 0.0f;
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st) {
+            const int c = 2 * st + half;
+            const bool kin = 8 * c < a.K;
+            qk_u32x4 kf[2];
+#pragma unroll
+            for (int y = 0; y < 2; ++y) kf[y] = kin ? lds_read16(kl + koff[y] + 16 * (c ^ ksw[y])) : zero;
+#pragma unroll
+            for (int x = 0; x < 2; ++x)
+#pragma unroll
+                for (int y = 0; y < 2; ++y) acc[x][y] = QkMfma<T>::run(kf[y], qf[x][st], acc[x][y]);
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): K block kb+1 has landed
+        __syncthreads();                      // ... for every wavefront; buffer `kl` is free for staging
+        // epilogue as in qk_score_mfma_kernel, with 32-bit lane offsets from the wavefront's
+        // block (the launcher checks that 64 rows and 64 columns of strides fit)
+        const int64_t j0 = kb * kMfmaBlock + (wave & 1) * 64;
+        qk_lds_u8* stg = kl + wave * 32 * 256;
+        const int col = 4 * (lane & 15);
+        const int64_t jb = j0 + col;
+        float* cw = a.c + bt * a.c_sb + i0 * a.c_sm + j0 * a.c_sn;
+        const int csm = (int)a.c_sm, csn = (int)a.c_sn;
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+#pragma unroll
+            for (int y = 0; y < 2; ++y)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int chunk = 8 * y + 2 * g + half;
+                    lds_write_f4(stg + r * 256 + 16 * (chunk ^ (r & 15)),
+                                 qk_f32x4{acc[x][y][4 * g], acc[x][y][4 * g + 1], acc[x][y][4 * g + 2],
+                                          acc[x][y][4 * g + 3]});
+                }
+            __syncthreads();
+            // two rows of stores per unrolled step: more would hoist every row's address out of
+            // the K-block loop and leave too few registers for two wavefronts per SIMD
+#pragma unroll 2
+            for (int it = 0; it < 8; ++it) {
+                const int row = 4 * it + (lane >> 4);
+                const int rr = 32 * x + row;   // row in the wavefront's block
+                if (i0 + rr >= a.M || jb >= a.N) continue;
+                const qk_f32x4 raw = lds_read_f4(stg + row * 256 + 16 * ((lane & 15) ^ (row & 15)));
+                float v[4] = {raw[0], raw[1], raw[2], raw[3]};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v[u] = a.has_scale ? v[u] * a.scale : v[u];
+                if (a.vec4 && jb + 3 < a.N) {
+                    *(float4*)(cw + (rr * csm + col)) = make_float4(v[0], v[1], v[2], v[3]);
+                } else {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        if (jb + u >= a.N) break;
+                        cw[rr * csm + (col + u) * csn] = v[u];
+                    }
+                }
+            }
+            __syncthreads();  // the next pass (or the next K block's copy) reuses the buffer
+        }
+    }
+}
+
+// K blocks per workgroup of the row kernel: runs of 4, shorter where that would
+// leave fewer than one round of workgroups (two per CU on 256 CUs), longer
+// beyond 4096 workgroups. Measured on 32 heads x D 128: 1024^2 0.029 ms with 4
+// (0.033 with 2, 0.040 with 1 or 8), 2048^2 0.124 ms with 4 (0.164 with 8 or
+// 16), 4096^2 0.463-0.465 ms with 8 or 16 (0.513 with 32).
+inline int64_t rows_blocks_per_workgroup(int64_t tiles, int64_t nkb) {
+    int64_t tpw = tiles / 4096;
+    if (tpw < 4) tpw = std::min<int64_t>(4, std::max<int64_t>(1, tiles / 512));
+    return std::min(tpw, nkb);
+}
+
 }  // namespace
 
 bool qk_score_mfma_supported(const QkScoreArgs& a, int dtype) {
@@ -295,6 +460,41 @@ hipError_t launch_qk_score_mfma(const QkScoreArgs& a, int dtype, hipStream_t s) 
     const bool c_vec = a.c_sn == 1 && a.c_sm % 4 == 0 && a.c_sb % 4 == 0 && al16(a.c);
     const bool b_vec = a.bias == nullptr ||
                        (a.bias_sn == 1 && a.bias_sm % 4 == 0 && a.bias_sb % 4 == 0 && al16(a.bias));
+    // Scores only (no bias, no soft-cap), K <= 128, lane offsets within 32 bits: the row kernel.
+    const int64_t lim31 = int64_t(1) << 31;
+    const bool rows = a.bias == nullptr && !(a.softcap > 0.0f) && a.K <= 128 &&
+                      (kMfmaBlock - 1) * a.b_sn + a.K < lim31 && 63 * (a.c_sm + a.c_sn) + 4 < lim31 &&
+                      a.b_sn >= 0 && a.c_sm >= 0 && a.c_sn >= 0;
+    if (rows) {
+        const int64_t nqb = (a.M + kMfmaBlock - 1) / kMfmaBlock, nkb = (a.N + kMfmaBlock - 1) / kMfmaBlock;
+        const int64_t max_grid = (int64_t(1) << 31) - 1;
+        for (int64_t b0 = 0; b0 < a.batch;) {
+            QkScoreArgs x = a;
+            x.vec4 = c_vec;
+            x.batch = std::min<int64_t>(a.batch - b0, std::max<int64_t>(1, max_grid / (nqb * nkb)));
+            x.q = (const char*)a.q + b0 * a.a_sb * 2;
+            x.k = (const char*)a.k + b0 * a.b_sb * 2;
+            x.c = a.c + b0 * a.c_sb;
+            const int64_t tiles = x.batch * nqb * nkb;
+            const int64_t tpw = rows_blocks_per_workgroup(tiles, nkb);
+            const int64_t npieces = (nkb + tpw - 1) / tpw;
+            const dim3 grid((unsigned)(x.batch * nqb * npieces));
+            const int K = (int)a.K;
+            if (dtype == DT_BF16) {
+                if (K <= 32) hipLaunchKernelGGL((qk_score_mfma_rows_kernel<__bf16, 4>), grid, dim3(256), 0, s, x, nqb, npieces, (int)tpw);
+                else if (K <= 64) hipLaunchKernelGGL((qk_score_mfma_rows_kernel<__bf16, 8>), grid, dim3(256), 0, s, x, nqb, npieces, (int)tpw);
+                else hipLaunchKernelGGL((qk_score_mfma_rows_kernel<__bf16, 16>), grid, dim3(256), 0, s, x, nqb, npieces, (int)tpw);
+            } else {
+                if (K <= 32) hipLaunchKernelGGL((qk_score_mfma_rows_kernel<_Float16, 4>), grid, dim3(256), 0, s, x, nqb, npieces, (int)tpw);
+                else if (K <= 64) hipLaunchKernelGGL((qk_score_mfma_rows_kernel<_Float16, 8>), grid, dim3(256), 0, s, x, nqb, npieces, (int)tpw);
+                else hipLaunchKernelGGL((qk_score_mfma_rows_kernel<_Float16, 16>), grid, dim3(256), 0, s, x, nqb, npieces, (int)tpw);
+            }
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            b0 += x.batch;
+        }
+        return hipSuccess;
+    }
     for (int64_t b0 = 0; b0 < a.batch; b0 += kMaxGridZ) {
         QkScoreArgs x = a;
         x.vec4 = c_vec && b_vec;

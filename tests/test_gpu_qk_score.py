@@ -163,6 +163,33 @@ def test_mfma_kernel_within_bound(ofh, dt, shape):
         assert excess.max() <= 0, f"max excess {excess.max():.3e}"
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("shape", [(1, 64, 64, 32), (2, 130, 257, 64), (3, 200, 328, 72), (2, 384, 1030, 128),
+                                   (8, 1000, 9000, 72), (8, 1024, 10240, 64)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_mfma_row_kernel_matches_block_kernel(ofh, dt, shape):
+    """Without a bias (K <= 128) the scores come from the pipelined row kernel
+    (Q fragments in registers, a run of 128-key blocks per workgroup, the
+    larger shapes with two blocks per run and a ragged last run); with an
+    all-zero bias from the one-block kernel. Same products and summation order,
+    so the values are equal (x + 0 only turns -0 into +0), also into a strided
+    output whose rows are not 16-byte aligned."""
+    T, M, N, D = shape
+    rng = np.random.default_rng(M + N + D)
+    tq, _ = to_device(rng.standard_normal((T, M, D), dtype=np.float32), dt)
+    tk, _ = to_device(rng.standard_normal((T, N, D), dtype=np.float32), dt)
+    zero = torch.zeros((T, M, N), dtype=torch.float32, device="cuda")
+    print(f"row kernel {dt} {shape}", flush=True)
+    rows = _run(ofh, tq, tk, scale=0.125, algorithm=ofh.QK_MFMA)
+    block = _run(ofh, tq, tk, scale=0.125, bias=zero, algorithm=ofh.QK_MFMA)
+    assert torch.equal(rows, block)
+    if M * N <= 1 << 20:
+        strided = torch.full((T, M, N + 1), float("nan"), dtype=torch.float32, device="cuda")[:, :, :N]
+        _run(ofh, tq, tk, scale=None, out=strided, algorithm=ofh.QK_MFMA)
+        plain = _run(ofh, tq, tk, scale=None, bias=zero, algorithm=ofh.QK_MFMA)
+        assert torch.equal(strided, plain)
+
+
 def test_auto_picks_mfma_for_16bit_and_exact_for_fp32(ofh):
     rng = np.random.default_rng(2)
     tq, uq = to_device(rng.standard_normal((2, 96, 64), dtype=np.float32), "bf16")
