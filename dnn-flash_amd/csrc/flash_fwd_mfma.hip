@@ -435,6 +435,7 @@ __device__ void merge_split_rows(const FwdArgs& a, int bh, int q0, int rows, int
 constexpr int kBlockN16 = 64;      // keys per K/V tile (16-bit kernels) ...
 constexpr int kBlockN16Wide = 128; // ... and for D = 64 without score_mod or block mask
 constexpr float kRescaleSlack = 8.0f;
+constexpr float kSumBound = 256.0f;  // 2^kRescaleSlack
 constexpr int kFragAhead = 4;  // LDS fragment reads in flight ahead of the MFMAs (plain scale)
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
@@ -887,6 +888,30 @@ struct Wave32 {
         const bool need_mask = tile_crosses(kt) || (LIST && !list_full(e_ent, wave));
         float mx = kNegInf;
         const bool raw = MOD == MOD_PLAIN && !need_mask;  // s still holds raw dot products
+        // 128-key tiles (D <= 64, no list): p is taken against the running max
+        // first, without the tile's max. A row sum of at most 2^kRescaleSlack
+        // proves every p <= 2^kRescaleSlack, the bound the lazy rescale keeps,
+        // so the result is the one the max would have given (the max raises
+        // nothing then). Otherwise (a larger sum, inf or NaN) the tile is redone
+        // below with its max. Measured +4-7 % at D = 32 and 64; at D = 96 and
+        // 128 (64-key tiles) the same code measured 3-4 % slower.
+        if (D <= 64 && !LIST && raw && __builtin_amdgcn_ballot_w64(m_run == kNegInf) == 0) {
+            float fsum = 0.0f;
+#pragma unroll
+            for (int c = 0; c < BN / 16; ++c) {
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+                    pf[c][t] = (T)__builtin_amdgcn_exp2f(
+                        __builtin_fmaf(s[c >> 1][8 * (c & 1) + t], a.scale_log2, -m_run));
+#pragma unroll
+                for (int t = 0; t < 8; t += 2)
+                    fsum = Dot2<T>::sum2(typename Dot2<T>::v2{pf[c][t], pf[c][t + 1]}, fsum);
+            }
+            if (__builtin_amdgcn_ballot_w64(!(fsum <= kSumBound)) == 0) {
+                l_run += fsum;
+                return;
+            }
+        }
         const bool capped = MOD == MOD_GENERAL && a.softcap > 0.0f;  // uniform
         const float cap_hi = a.softcap * kLog2e, cap_m2 = -2.0f * a.softcap * kLog2e;
         if (raw) {

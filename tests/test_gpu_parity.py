@@ -567,6 +567,24 @@ def test_rescale_with_live_accumulator(ofh, dt, D, sign, splits):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("D", [32, 64])
+@pytest.mark.parametrize("splits", [1, 0])
+def test_row_sum_bound_without_raise(ofh, dt, D, splits):
+    """128-key tiles take p against the running max and keep it only when the
+    row sum proves p <= 2^8. Region S1 at +5 log2 units (below the slack of 8)
+    makes that sum exceed 2^8 with no p above 2^8: the tile is redone with its
+    max, which raises nothing. S2 (+14.5) still raises it, and a negative scale
+    takes the min-based max of the redo."""
+    N = 2048
+    for sign in (1.0, -1.0):
+        for causal, M in ((False, 300), (True, N)):
+            dev, host, scale = rescale_inputs(dt, 1, 2, M, N, D, seed=D + 5, sign=sign, d1=5.0)
+            out = run(ofh, dev, dt=dt, causal=causal, scale=scale, max_key_splits=splits)
+            ref = oracle_full(host, causal=causal, scale=scale)
+            check(out, ref, dt, f"{dt} D{D} sum bound causal={causal} scale={scale:+.4f} max_key_splits={splits}")
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("sign", [1.0, -1.0])
 @pytest.mark.parametrize("splits", [1, 0])
 def test_rescale_with_live_accumulator_block_mask(ofh, dt, sign, splits):
