@@ -137,11 +137,13 @@ int validate(const ofh_attention_params* p, bool check_ptrs, const void* q, cons
 // remove steps, so the unmasked count is an upper bound.
 // Workgroups that run at once per CU for the kernel the call takes (registers
 // and LDS of the kernels in flash_fwd_mfma.hip): the 8-wavefront 16-bit
-// kernels one, the 4-wavefront ones two up to D = 128, the fp32 kernels two up
-// to D = 64.
+// kernels one, the 4-wavefront ones two up to D = 128 (three for the
+// plain-scale block-mask kernels up to D = 64), the fp32 kernels two up to
+// D = 64.
 int workgroups_per_cu(const ofh_attention_params* p, const Resolved& r) {
     if (p->dtype == OFH_DTYPE_F32) return p->head_dim <= 64 ? 2 : 1;
     if (r.threads >= 512) return 1;
+    if (r.tile_list && !r.general_mod && p->head_dim <= 64) return 3;
     return p->head_dim < 160 ? 2 : 1;
 }
 constexpr int64_t kComputeUnits = 256;  // MI355X

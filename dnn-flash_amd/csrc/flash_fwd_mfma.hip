@@ -1327,11 +1327,18 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
 
 // Workgroups per CU the register budget is sized for: one of 8 wavefronts,
 // two of 4, or one of 4 from D = 160 up (one wavefront per SIMD, so the O
-// accumulators can use the accumulation registers).
-constexpr int lockstep_min_blocks(int D, int nwaves) { return nwaves == 8 ? 1 : (D >= 160 ? 1 : 2); }
+// accumulators can use the accumulation registers). The plain-scale
+// block-mask kernels at D <= 64 fit three of 4 (at most 168 VGPRs: 163 at
+// D = 64, 128 at D = 32, no spills; their LDS, three 16 KB stages and the
+// list, fits three workgroups too): the third wavefront per SIMD measured
+// +2-4 % on the fp16 block-sparse workload. With a score_mod the same bound
+// spills, so those keep two.
+constexpr int lockstep_min_blocks(int D, int nwaves, int mod, bool list) {
+    return nwaves == 8 ? 1 : D >= 160 ? 1 : (list && mod == MOD_PLAIN && D <= 64) ? 3 : 2;
+}
 
 template <typename T, int D, int MOD, bool LIST, int NWAVES, bool PAIRED, int BN = kBlockN16, int SB = 1>
-__global__ __launch_bounds__(NWAVES * 64, lockstep_min_blocks(D, NWAVES)) void flash_fwd_lockstep_kernel(FwdArgs a) {
+__global__ __launch_bounds__(NWAVES * 64, lockstep_min_blocks(D, NWAVES, MOD, LIST)) void flash_fwd_lockstep_kernel(FwdArgs a) {
     using L = TileLayout<D, BN * SB>;
     // block-mask kernels: LDS sized at launch (list_kernel_lds_bytes)
     extern __shared__ __attribute__((aligned(16))) unsigned char dyn_smem[];
