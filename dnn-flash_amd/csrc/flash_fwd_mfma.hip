@@ -893,8 +893,8 @@ struct Wave32 {
         // proves every p <= 2^kRescaleSlack, the bound the lazy rescale keeps,
         // so the result is the one the max would have given (the max raises
         // nothing then). Otherwise (a larger sum, inf or NaN) the tile is redone
-        // below with its max. Measured +4-7 % at D = 32 and 64; at D = 96 and
-        // 128 (64-key tiles) the same code measured 3-4 % slower.
+        // below with its max. Measured +5-6 % at D = 32 and 64; at D = 96 and
+        // 128 (64-key tiles) the same code measured slower (3-6 %).
         if (D <= 64 && !LIST && raw && __builtin_amdgcn_ballot_w64(m_run == kNegInf) == 0) {
             float fsum = 0.0f;
 #pragma unroll
@@ -1330,9 +1330,10 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
 // accumulators can use the accumulation registers). The plain-scale
 // block-mask kernels at D <= 64 fit three of 4 (at most 168 VGPRs: 163 at
 // D = 64, 128 at D = 32, no spills; their LDS, three 16 KB stages and the
-// list, fits three workgroups too): the third wavefront per SIMD measured
-// +2-4 % on the fp16 block-sparse workload. With a score_mod the same bound
-// spills, so those keep two.
+// list, fits three workgroups too). On the fp16 block-sparse workload the
+// third wavefront per SIMD measured within 1 % of two (+0.1 to +0.6 % with
+// the timing order alternated). With a score_mod the same bound spills, so
+// those keep two.
 constexpr int lockstep_min_blocks(int D, int nwaves, int mod, bool list) {
     return nwaves == 8 ? 1 : D >= 160 ? 1 : (list && mod == MOD_PLAIN && D <= 64) ? 3 : 2;
 }
