@@ -48,6 +48,7 @@ struct Resolved {
     int num_q_tiles, num_k_tiles;
     int key_splits;      // workgroups per query tile, each over a range of K/V tiles
     int split_tiles;     // K/V tile steps per split
+    bool pair_split;     // fp32 causal: query tile pairs, each tile split in key_splits ranges of its own length
 };
 
 void contiguous_strides(int64_t out[3], const int64_t in[3], size_t H, size_t T, size_t last) {
@@ -160,12 +161,31 @@ constexpr int64_t kComputeUnits = 256;  // MI355X
 void choose_key_splits(const ofh_attention_params* p, Resolved& r) {
     r.key_splits = 1;
     r.split_tiles = 1 << 30;
+    r.pair_split = false;
     if (p->dtype == OFH_DTYPE_F32 && r.paired) return;
     if (p->max_key_splits == 1) return;
     const bool rows32 = p->dtype == OFH_DTYPE_F32 && r.block_m == ofh::kRowsF32;
     const int64_t slots = kComputeUnits * workgroups_per_cu(p, r);
     const int kMaxSplits = p->max_key_splits > 1 ? std::min(p->max_key_splits, 64) : 64;
     const int64_t bh = (int64_t)p->batch * p->heads;
+    // fp32 causal, 128-row tiles: query tiles p and nqt-1-p share a workgroup
+    // and every tile is cut into S ranges of its own length, so all workgroups
+    // run about the same number of steps; S is the largest count whose pairs
+    // fit one round of the slots. Measured on fp32 causal B2 H8 N2048 D64 (128
+    // pairs, S = 4): see the design notes; a common range length for all
+    // tiles (3 splits of 11 steps) left the shorter tiles' workgroups idle.
+    if (p->dtype == OFH_DTYPE_F32 && !rows32 && p->causal && !r.tile_list) {
+        const int64_t pairs = bh * ((r.num_q_tiles + 1) / 2);
+        const int64_t kend = std::min<int64_t>((int64_t)p->key_tokens, (int64_t)r.num_q_tiles * r.block_m);
+        const int64_t max_steps = (kend + r.block_n - 1) / r.block_n;
+        const int64_t s = std::min<int64_t>({(int64_t)kMaxSplits, slots / std::max<int64_t>(pairs, 1), max_steps});
+        if (s >= 2) {
+            r.paired = true;
+            r.pair_split = true;
+            r.key_splits = (int)s;
+            return;
+        }
+    }
     const int64_t wgs = bh * (r.paired ? (r.num_q_tiles + 1) / 2 : r.num_q_tiles);
     if (wgs >= slots) return;
     // tile steps of each query tile (block_n keys each)
@@ -214,6 +234,7 @@ void set_lds_list(const ofh_attention_params* p, Resolved& r) {
 void no_key_split(const ofh_attention_params* p, Resolved& r) {
     r.key_splits = 1;
     r.split_tiles = 1 << 30;
+    r.pair_split = false;
     if (p->dtype == OFH_DTYPE_F32 && r.block_m == ofh::kRowsF32) return;  // 32-row blocks: no pairing, no list
     const ofh::MfmaTiles t =
         ofh::flash_mfma_tiles(p->dtype, (int)p->head_dim, r.general_mod, r.tile_list, p->causal != 0);
@@ -266,6 +287,7 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
         r.num_k_tiles = 0;
         r.key_splits = 1;
         r.split_tiles = 1 << 30;
+        r.pair_split = false;
         return OFH_SUCCESS;
     }
     r.algorithm = OFH_ALGO_FLASH_MFMA;
@@ -503,6 +525,7 @@ int fwd_impl(const ofh_attention_params* p, const void* q, const void* k, const 
     }
     a.num_splits = r.key_splits;
     a.split_tiles = r.split_tiles;
+    a.pair_split = r.pair_split ? 1 : 0;
     a.split_bm = r.block_m;
     a.split_bn = r.block_n;
     if (r.key_splits > 1) {

@@ -227,15 +227,20 @@ __device__ __forceinline__ float online_softmax_tile(const FwdArgs& a, f32x16 (&
 // ---------------------------------------------------------------------------
 // Key split (FwdArgs::num_splits > 1). Query tile qt has steps(qt) K/V tile
 // steps; splits [0, active(qt)) of it run, split s over steps
-// [s*split_tiles, (s+1)*split_tiles). With one active split, split 0 writes O
+// [s*range, (s+1)*range), range = split_range(steps(qt)). With one active split, split 0 writes O
 // directly. Otherwise every active split writes its unnormalised partial rows
 // (O_s, m_s, l_s) and the rows are merged with the log-sum-exp rule of
 // attention.cpp:661-674 applied across splits:
 //   m* = max_s m_s,  O = sum_s 2^(m_s - m*) O_s / sum_s 2^(m_s - m*) l_s.
 // Rows that saw no valid key in any split (l = 0) are written as 0.
 
+// Steps per split of a query tile with `steps` K/V tile steps.
+__device__ __forceinline__ int split_range(const FwdArgs& a, int steps) {
+    return a.pair_split ? max(1, (steps + a.num_splits - 1) / a.num_splits) : a.split_tiles;
+}
 __device__ __forceinline__ int split_active(const FwdArgs& a, int steps) {
-    return max(1, min(a.num_splits, (steps + a.split_tiles - 1) / a.split_tiles));
+    const int range = split_range(a, steps);
+    return max(1, min(a.num_splits, (steps + range - 1) / range));
 }
 
 // Folds partial (m2, l2, o2) into (m, l, o); maxima in log2 units.
@@ -1369,7 +1374,11 @@ __global__ __launch_bounds__(NWAVES * 64, lockstep_min_blocks(D, NWAVES, MOD, LI
 // and each PV step takes the two keys that the lane halves hold in register u.
 // With a key split (FwdArgs::num_splits > 1) the workgroups of a query tile
 // each run a range of its K/V tile steps and write partial rows, which
-// combine_splits_kernel merges.
+// combine_splits_kernel merges. Causal calls split with FwdArgs::pair_split:
+// workgroup s of the pair (nqt-1-p, p) runs split s of both query tiles, each
+// tile cut into num_splits ranges of its own length, so a workgroup runs
+// about (steps(nqt-1-p) + steps(p)) / num_splits steps whatever p is (with
+// one range length for all tiles the longest tile's ranges set the time).
 
 constexpr int kBlockNF32 = 32;  // keys per accumulator block of the fp32 kernel
 constexpr int kTilesF32 = 2;    // blocks per K/V tile: 64 keys per barrier (+3 to +5 % over one block)
@@ -1377,27 +1386,32 @@ constexpr int kWaves32 = 4;
 constexpr int kThreads32 = kWaves32 * 64;
 constexpr int kBlockM32 = kWaves32 * kQueriesPerWave;  // 128
 
-template <int D, bool GENERAL, int NB = 1>
-__global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a) {
-    constexpr int BN = kBlockNF32 * NB;  // NB blocks of 32 keys per K/V tile
-    constexpr int KSTR = D + 4;  // floats; conflict-free 16-byte reads of rows kappa(r)
-    constexpr int VSTR = D + 4;  // floats; lane halves read rows 8 apart -> opposite bank halves
-    constexpr int KTILE = BN * KSTR;
-    constexpr int STAGE = 2 * KTILE;
+template <int D, int NB>
+struct Mfma32Tiles {
+    static constexpr int BN = kBlockNF32 * NB;  // NB blocks of 32 keys per K/V tile
+    static constexpr int KSTR = D + 4;  // floats; conflict-free 16-byte reads of rows kappa(r)
+    static constexpr int VSTR = D + 4;  // floats; lane halves read rows 8 apart -> opposite bank halves
+    static constexpr int KTILE = BN * KSTR;
+    static constexpr int STAGE = 2 * KTILE;
+};
+
+// Query tile qt of head bh, key split `split` (the whole key range without
+// one), on the workgroup's LDS `lds` (2 * STAGE floats).
+template <int D, bool GENERAL, int NB>
+__device__ __forceinline__ void mfma32_qtile(const FwdArgs& a, float* lds, int bh, int qt, int split) {
+    using TL = Mfma32Tiles<D, NB>;
+    constexpr int BN = TL::BN;
+    constexpr int KSTR = TL::KSTR;
+    constexpr int VSTR = TL::VSTR;
+    constexpr int KTILE = TL::KTILE;
+    constexpr int STAGE = TL::STAGE;
     constexpr int CHUNKS = BN * D / 4;
     constexpr int CPT = CHUNKS / kThreads32;
     constexpr int NDC = D / 4;
     static_assert(CHUNKS % kThreads32 == 0, "tile must split evenly over the workgroup");
 
-    __shared__ __attribute__((aligned(16))) float lds[2 * STAGE];
-
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5, r = lane & 31;
-
-    int bh, qt;
-    const int tiles_per_split = a.B * a.H * a.num_q_tiles;
-    const int split = (int)blockIdx.x / tiles_per_split;
-    map_work((int)blockIdx.x - split * tiles_per_split, a.B * a.H, a.num_q_tiles, a.causal, bh, qt);
     const int b = bh / a.H, h = bh - b * a.H;
     const float* __restrict__ Qp = (const float*)a.q + b * a.q_sb + h * a.q_sh;
     const float* __restrict__ Kp = (const float*)a.k + b * a.k_sb + h * a.k_sh;
@@ -1430,8 +1444,9 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a)
     // tile steps [it0, it1) of this workgroup's key split
     const int active = split_active(a, ntiles);
     if (split >= active) return;  // uniform over the workgroup
-    const int it0 = split * a.split_tiles;
-    const int it1 = min(ntiles, it0 + a.split_tiles);
+    const int range = split_range(a, ntiles);
+    const int it0 = split * range;
+    const int it1 = min(ntiles, it0 + range);
 
     f32x4 kreg[CPT], vreg[CPT];
     auto load_tile = [&](int kt) {
@@ -1578,6 +1593,28 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a)
             }
         }
     }
+}
+
+template <int D, bool GENERAL, int NB = 1>
+__global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a) {
+    __shared__ __attribute__((aligned(16))) float lds[2 * Mfma32Tiles<D, NB>::STAGE];
+    if (a.pair_split) {  // causal query tile pairs, split s of both tiles
+        const int pairs = a.B * a.H * ((a.num_q_tiles + 1) / 2);
+        const int split = (int)blockIdx.x / pairs;
+        int bh, qa, qb;
+        map_work_pair((int)blockIdx.x - split * pairs, a.B * a.H, a.num_q_tiles, bh, qa, qb);
+        mfma32_qtile<D, GENERAL, NB>(a, lds, bh, qa, split);
+        if (qb >= 0) {
+            __syncthreads();  // LDS stages are reused
+            mfma32_qtile<D, GENERAL, NB>(a, lds, bh, qb, split);
+        }
+        return;
+    }
+    int bh, qt;
+    const int tiles_per_split = a.B * a.H * a.num_q_tiles;
+    const int split = (int)blockIdx.x / tiles_per_split;
+    map_work((int)blockIdx.x - split * tiles_per_split, a.B * a.H, a.num_q_tiles, a.causal, bh, qt);
+    mfma32_qtile<D, GENERAL, NB>(a, lds, bh, qt, split);
 }
 
 // fp32 calls with few query rows (latency-bound: fewer 128-row query tiles
@@ -1942,17 +1979,17 @@ hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipS
             }
         }
         if (a.D == 96)
-            return general_mod ? launch(flash_fwd_mfma32_kernel<96, true, kTilesF32>, kThreads32, a, s)
-                               : launch(flash_fwd_mfma32_kernel<96, false, kTilesF32>, kThreads32, a, s);
+            return general_mod ? launch(flash_fwd_mfma32_kernel<96, true, kTilesF32>, kThreads32, a, s, a.pair_split != 0)
+                               : launch(flash_fwd_mfma32_kernel<96, false, kTilesF32>, kThreads32, a, s, a.pair_split != 0);
         if (a.D == 32)
-            return general_mod ? launch(flash_fwd_mfma32_kernel<32, true, kTilesF32>, kThreads32, a, s)
-                               : launch(flash_fwd_mfma32_kernel<32, false, kTilesF32>, kThreads32, a, s);
+            return general_mod ? launch(flash_fwd_mfma32_kernel<32, true, kTilesF32>, kThreads32, a, s, a.pair_split != 0)
+                               : launch(flash_fwd_mfma32_kernel<32, false, kTilesF32>, kThreads32, a, s, a.pair_split != 0);
         if (a.D == 64)
-            return general_mod ? launch(flash_fwd_mfma32_kernel<64, true, kTilesF32>, kThreads32, a, s)
-                               : launch(flash_fwd_mfma32_kernel<64, false, kTilesF32>, kThreads32, a, s);
+            return general_mod ? launch(flash_fwd_mfma32_kernel<64, true, kTilesF32>, kThreads32, a, s, a.pair_split != 0)
+                               : launch(flash_fwd_mfma32_kernel<64, false, kTilesF32>, kThreads32, a, s, a.pair_split != 0);
         if (a.D == 128)
-            return general_mod ? launch(flash_fwd_mfma32_kernel<128, true, kTilesF32>, kThreads32, a, s)
-                               : launch(flash_fwd_mfma32_kernel<128, false, kTilesF32>, kThreads32, a, s);
+            return general_mod ? launch(flash_fwd_mfma32_kernel<128, true, kTilesF32>, kThreads32, a, s, a.pair_split != 0)
+                               : launch(flash_fwd_mfma32_kernel<128, false, kTilesF32>, kThreads32, a, s, a.pair_split != 0);
     }
     return hipErrorInvalidValue;
 }

@@ -238,9 +238,11 @@ def test_kernel_choice(ofh):
     # fp32 decode: one 32-row block per head, its 1024 tiles over 32 workgroups
     info = F.launch_info(F.make_params(1, 8, 1, 32768, 128, dtype=F.DTYPE_F32))
     assert info.block_m == 32 and info.key_splits == 32 and info.workgroups == 8 * 32
-    # fp32 causal B2 H8 N2048 (128-row tiles, two workgroups per CU): 3 splits
+    # fp32 causal B2 H8 N2048 (128-row tiles, two workgroups per CU): query
+    # tiles paired, each tile in 4 ranges of its own length: 128 pairs x 4
     p = F.make_params(2, 8, 2048, 2048, 64, dtype=F.DTYPE_F32, causal=True)
-    assert F.launch_info(p).key_splits == 3
+    info = F.launch_info(p)
+    assert info.key_splits == 4 and info.workgroups == 16 * 8 * 4
     p = F.make_params(8, 32, 2048, 2048, 64, dtype=F.DTYPE_F32, causal=True)
     assert F.launch_info(p).key_splits == 1 and F.workspace_bytes(p) == 0
     # K/V token strides beyond 2^24 elements: the rowwise kernel (64-bit offsets)

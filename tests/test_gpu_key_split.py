@@ -166,6 +166,32 @@ def test_split_block_mask_and_score_mod(ofh, dt):
     check(out.cpu().numpy(), O.standard_attention(uq, uk, uv, prob), dt, f"{dt} split score_mod")
 
 
+@pytest.mark.parametrize("shape", [(1, 8, 2048, 2048, 64), (1, 12, 1400, 1400, 64), (1, 16, 1024, 2048, 64),
+                                   (1, 8, 2048, 700, 64), (1, 8, 2048, 2048, 128), (2, 4, 2048, 2048, 32)])
+@pytest.mark.parametrize("cap", [0, 2])
+def test_fp32_causal_pair_split(ofh, shape, cap):
+    """fp32 causal calls of the 128-row kernel with a key split run query tiles
+    nqt-1-p and p in one workgroup and cut each tile into S ranges of its own
+    length (workgroup s runs split s of both): an even and an odd tile count
+    (the middle tile alone), M < N and M > N (top-left causal), D = 32/64/128,
+    and S = 2 (merged in the launch) or the planner's S (a second launch)."""
+    F = ofh
+    B, H, M, N, D = shape
+    p = F.make_params(B, H, M, N, D, dtype=DTYPE["f32"], causal=True, max_key_splits=cap)
+    info = F.launch_info(p)
+    nqt = -(-M // 128)
+    print(f"f32 causal {shape} cap={cap}: block_m {info.block_m} key_splits {info.key_splits} "
+          f"workgroups {info.workgroups} merge_in_launch {info.merge_in_launch}", flush=True)
+    assert info.block_m == 128 and info.key_splits >= 2
+    assert info.workgroups == B * H * ((nqt + 1) // 2) * info.key_splits
+    if cap == 2:
+        assert info.key_splits == 2
+    dev, host = make_inputs("f32", B, H, M, N, D, seed=M + N + D + cap)
+    ref = oracle_rows(host, True, 1.0 / math.sqrt(D))
+    out = fwd(F, dev, "f32", True, "f32", max_key_splits=cap).cpu().numpy()
+    check(out, ref, "f32", f"f32 causal pair split {shape} splits {info.key_splits}")
+
+
 def test_max_key_splits(ofh):
     """max_key_splits caps the split (1: none) and every cap gives the oracle's rows."""
     F = ofh
