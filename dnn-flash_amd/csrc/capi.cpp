@@ -168,24 +168,31 @@ void choose_key_splits(const ofh_attention_params* p, Resolved& r) {
     const int64_t slots = kComputeUnits * workgroups_per_cu(p, r);
     const int kMaxSplits = p->max_key_splits > 1 ? std::min(p->max_key_splits, 64) : 64;
     const int64_t bh = (int64_t)p->batch * p->heads;
-    // fp32 causal, 128-row tiles: query tiles p and nqt-1-p share a workgroup
-    // and every tile is cut into S ranges of its own length, so all workgroups
-    // run about the same number of steps; S is the largest count whose pairs
-    // fit one round of the slots. Measured on fp32 causal B2 H8 N2048 D64 (128
-    // pairs, S = 4): see the design notes; a common range length for all
-    // tiles (3 splits of 11 steps) left the shorter tiles' workgroups idle.
-    if (p->dtype == OFH_DTYPE_F32 && !rows32 && p->causal && !r.tile_list) {
+    // Causal calls without a block mask (fp32 on 128-row tiles, 16-bit):
+    // query tiles p and nqt-1-p share a workgroup and every tile is cut into S
+    // ranges of its own length, so all workgroups run about the same number of
+    // steps; S is the largest count whose pairs fit one round of the slots.
+    // fp32 takes it first: a common range length for all tiles (causal B2 H8
+    // N2048 D64: 3 splits of 11 steps) left the shorter tiles' workgroups idle.
+    // 16-bit calls take it only where the common ranges would not split (the
+    // pairs alone then leave CUs idle: f16 causal B1 H8 N8192 D128 0.223 ->
+    // 0.172 ms); where they do split, a second tile per workgroup (its
+    // prologue, partial rows and a wider merge) measured slower (bf16 causal
+    // B1 H8 N4096 D128: 3 common ranges 0.060 ms, 4 per-tile ranges 0.065).
+    const bool pair_ok = !rows32 && p->causal && !r.tile_list;
+    auto pair_split = [&]() {
         const int64_t pairs = bh * ((r.num_q_tiles + 1) / 2);
         const int64_t kend = std::min<int64_t>((int64_t)p->key_tokens, (int64_t)r.num_q_tiles * r.block_m);
         const int64_t max_steps = (kend + r.block_n - 1) / r.block_n;
         const int64_t s = std::min<int64_t>({(int64_t)kMaxSplits, slots / std::max<int64_t>(pairs, 1), max_steps});
-        if (s >= 2) {
-            r.paired = true;
-            r.pair_split = true;
-            r.key_splits = (int)s;
-            return;
-        }
-    }
+        if (s < 2) return false;
+        r.paired = true;
+        r.pair_split = true;
+        r.key_splits = (int)s;
+        r.split_tiles = 1 << 30;
+        return true;
+    };
+    if (pair_ok && p->dtype == OFH_DTYPE_F32 && pair_split()) return;
     const int64_t wgs = bh * (r.paired ? (r.num_q_tiles + 1) / 2 : r.num_q_tiles);
     if (wgs >= slots) return;
     // tile steps of each query tile (block_n keys each)
@@ -218,7 +225,10 @@ void choose_key_splits(const ofh_attention_params* p, Resolved& r) {
     }
     const int per = per_of(lo);
     const int splits = (max_steps + per - 1) / per;
-    if (splits <= 1) return;
+    if (splits <= 1) {
+        if (pair_ok) pair_split();
+        return;
+    }
     r.key_splits = splits;
     r.split_tiles = per;
     r.paired = false;
@@ -744,6 +754,13 @@ int ofh_attention_launch_info(const ofh_attention_params* p, ofh_launch_info* in
         name = (p->dtype == OFH_DTYPE_F32 && r.block_m == ofh::kRowsF32)
                    ? rows32_kernel_name((int)p->head_dim, r.general_mod)
                    : ofh::flash_mfma_kernel_name(p->dtype, (int)p->head_dim, r.general_mod, r.tile_list);
+        // 16-bit causal pairs with a key split run the same tiling in a kernel of their own
+        static thread_local std::string pair_name;
+        const std::string lockstep = "flash_fwd_lockstep_kernel";
+        if (r.pair_split && p->dtype != OFH_DTYPE_F32 && std::string(name).compare(0, lockstep.size(), lockstep) == 0) {
+            pair_name = "flash_fwd_pair_split_kernel" + std::string(name).substr(lockstep.size());
+            name = pair_name.c_str();
+        }
     } else {
         info->block_m = 1;
         info->block_n = 64;

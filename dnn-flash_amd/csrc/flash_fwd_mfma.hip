@@ -1238,8 +1238,9 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
         const int nst = (kend + W::SN - 1) / W::SN;      // staged tiles
         const int active = SPLIT ? split_active(a, nst) : 1;
         if (split >= active) return;                     // uniform over the workgroup
-        const int st0 = SPLIT ? split * a.split_tiles : 0;
-        const int st1 = SPLIT ? min(nst, st0 + a.split_tiles) : nst;
+        const int range = SPLIT ? split_range(a, nst) : nst;
+        const int st0 = SPLIT ? split * range : 0;
+        const int st1 = SPLIT ? min(nst, st0 + range) : nst;
         W w(a, smem, bh, q0, wave);
         if (st0 >= st1) {  // uniform over the workgroup
             finish_qtile<W, NTHREADS, SPLIT>(a, w, smem, bh, qt, q0, BLOCK_M, split, active);
@@ -1291,8 +1292,9 @@ __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* 
     tile_range(a, qt, BLOCK_M, BN, ntiles, list);
     const int active = SPLIT ? split_active(a, ntiles) : 1;
     if (split >= active) return;  // uniform over the workgroup
-    const int it0 = SPLIT ? split * a.split_tiles : 0;
-    const int it1 = SPLIT ? min(ntiles, it0 + a.split_tiles) : ntiles;
+    const int range = SPLIT ? split_range(a, ntiles) : ntiles;
+    const int it0 = SPLIT ? split * range : 0;
+    const int it1 = SPLIT ? min(ntiles, it0 + range) : ntiles;
     W w(a, smem, bh, q0, wave);
     w.ntiles = ntiles;
     w.list = list;
@@ -1364,6 +1366,26 @@ __global__ __launch_bounds__(NWAVES * 64, lockstep_min_blocks(D, NWAVES, MOD, LI
     if (n > 1) {
         __syncthreads();  // LDS stages are reused
         lockstep_qtile<T, D, MOD, LIST, NWAVES, BN, SB, false>(a, smem, bh, qts[1]);
+    }
+}
+
+// Causal query tile pairs with a key split (FwdArgs::pair_split): workgroup s
+// of the pair (nqt-1-p, p) runs split s of both tiles, each tile cut into
+// num_splits ranges of its own length, so every workgroup runs about
+// (steps(nqt-1-p) + steps(p)) / num_splits staged tiles. A kernel of its own,
+// so that the paired kernel without a split keeps its code.
+template <typename T, int D, int MOD, int NWAVES, int BN = kBlockN16, int SB = 1>
+__global__ __launch_bounds__(NWAVES * 64, lockstep_min_blocks(D, NWAVES, MOD, false)) void flash_fwd_pair_split_kernel(FwdArgs a) {
+    using L = TileLayout<D, BN * SB>;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[2 * L::STAGE];
+    const int pairs = a.B * a.H * ((a.num_q_tiles + 1) / 2);
+    const int split = (int)blockIdx.x / pairs;
+    int bh, qa, qb;
+    map_work_pair((int)blockIdx.x - split * pairs, a.B * a.H, a.num_q_tiles, bh, qa, qb);
+    lockstep_qtile<T, D, MOD, false, NWAVES, BN, SB, true>(a, smem, bh, qa, split);
+    if (qb >= 0) {
+        __syncthreads();  // LDS stages are reused
+        lockstep_qtile<T, D, MOD, false, NWAVES, BN, SB, true>(a, smem, bh, qb, split);
     }
 }
 
@@ -1929,7 +1951,11 @@ static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
         return general_mod ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, true, 4, false>, 256, a, s, false, lds)
                            : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, true, 4, false>, 256, a, s, false, lds);
     }
+    const bool pair_split = a.pair_split != 0;
     if constexpr (D > 160) {
+        if (pair_split)
+            return general_mod ? launch(flash_fwd_pair_split_kernel<T, D, MOD_GENERAL, 4>, 256, a, s, true)
+                               : launch(flash_fwd_pair_split_kernel<T, D, MOD_PLAIN, 4>, 256, a, s, true);
         if (general_mod)
             return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 4, true>, 256, a, s, true)
                           : launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 4, false>, 256, a, s);
@@ -1939,11 +1965,13 @@ static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
         // score_mod: 64-key compute steps (two per staged tile at D = 32, 96, 160)
         constexpr int GSB = (D == 32 || (D & (D - 1)) != 0) ? 2 : 1;
         if (general_mod)
-            return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8, true, kBlockN16, GSB>, 512, a, s, true)
+            return pair_split ? launch(flash_fwd_pair_split_kernel<T, D, MOD_GENERAL, 8, kBlockN16, GSB>, 512, a, s, true)
+                 : paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8, true, kBlockN16, GSB>, 512, a, s, true)
                           : launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8, false, kBlockN16, GSB>, 512, a, s);
         // D <= 64: 128-key tiles; D = 128: 128 keys staged per barrier, two 64-key compute steps
         constexpr int BN = D <= 64 ? kBlockN16Wide : kBlockN16;
         constexpr int SB = D <= 64 ? 1 : kBlockN16Wide / kBlockN16;
+        if (pair_split) return launch(flash_fwd_pair_split_kernel<T, D, MOD_PLAIN, 8, BN, SB>, 512, a, s, true);
         return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, true, BN, SB>, 512, a, s, true)
                       : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, false, BN, SB>, 512, a, s);
     }

@@ -221,6 +221,11 @@ def test_kernel_choice(ofh):
     # tiles), 3 splits of 11: 256 workgroups with steps to run
     info = F.launch_info(F.make_params(1, 8, 4096, 4096, 128, dtype=F.DTYPE_BF16, causal=True))
     assert info.key_splits == 3 and info.workgroups == 8 * 16 * 3
+    # where those common ranges would not split (256 query tiles for 256 CUs,
+    # 128 pairs): the pairs, each tile in 2 ranges of its own length
+    info = F.launch_info(F.make_params(1, 8, 8192, 8192, 128, dtype=F.DTYPE_F16, causal=True))
+    assert info.key_splits == 2 and info.workgroups == 8 * 16 * 2
+    assert info.kernel_name.decode().startswith("flash_fwd_pair_split_kernel")
     info = F.launch_info(F.make_params(4, 32, 4096, 4096, 128, dtype=F.DTYPE_BF16))
     assert info.workgroups == 4 * 32 * 16
     assert info.key_splits == 1 and info.block_n == 128   # staged keys per barrier (2 x 64 computed)

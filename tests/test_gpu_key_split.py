@@ -192,6 +192,46 @@ def test_fp32_causal_pair_split(ofh, shape, cap):
     check(out, ref, "f32", f"f32 causal pair split {shape} splits {info.key_splits}")
 
 
+@pytest.mark.parametrize("case", [("bf16", 1, 32, 2048, 2048, 128, {}), ("f16", 1, 20, 2800, 2800, 64, {}),
+                                  ("bf16", 1, 64, 1024, 3000, 128, {}), ("f16", 1, 20, 3000, 1000, 128, {}),
+                                  ("bf16", 1, 32, 2048, 2048, 96, {}), ("bf16", 1, 16, 2048, 2048, 256, {}),
+                                  ("bf16", 1, 64, 1024, 1024, 128, {"softcap": 30.0, "alibi": True})])
+def test_16bit_causal_pair_split(ofh, case):
+    """16-bit causal calls whose query tiles would not split by a common range
+    (about one CU's worth of tiles) run flash_fwd_pair_split_kernel: query
+    tiles nqt-1-p and p in one workgroup, each cut into S ranges of its own
+    length, workgroup s running split s of both (an odd tile count leaves the
+    middle tile alone). Covers M < N and M > N (top-left causal), D = 64, 96,
+    128 and 256 (4 wavefronts), and ALiBi + soft-cap."""
+    F = ofh
+    dt, B, H, M, N, D, kw = case
+    kw = dict(kw)
+    alibi = kw.pop("alibi", False)
+    p = F.make_params(B, H, M, N, D, dtype=DTYPE[dt], causal=True, **kw)
+    info = F.launch_info(p)
+    print(f"{case}: {info.kernel_name.decode()} block_m {info.block_m} key_splits {info.key_splits} "
+          f"workgroups {info.workgroups} merge_in_launch {info.merge_in_launch}", flush=True)
+    nqt = -(-M // info.block_m)
+    assert info.key_splits >= 2 and info.kernel_name.decode().startswith("flash_fwd_pair_split_kernel")
+    assert info.workgroups == B * H * ((nqt + 1) // 2) * info.key_splits
+    dev, host = make_inputs(dt, B, H, M, N, D, seed=M + N + D)
+    uq, uk, uv = host
+    scale = 1.0 / math.sqrt(D)
+    slopes = None
+    if alibi:
+        slopes = (2.0 ** (-8.0 * np.arange(1, H + 1) / H)).astype(np.float32)
+        kw["alibi_slopes"] = torch.from_numpy(slopes).cuda()
+    out = fwd(F, dev, dt, True, "f32", **kw).cpu().numpy()
+    if alibi or "softcap" in kw:
+        prob = O.Problem(B, H, M, N, D, D, scale=scale, causal=True, alibi_slopes=slopes, softcap=kw.get("softcap", 0.0))
+        head_idx = np.repeat(np.arange(B * H, dtype=np.uint64), M)
+        rows = np.tile(np.arange(M, dtype=np.uint64), B * H)
+        ref = O.standard_attention_rows(uq, uk, uv, prob, head_idx, rows, threads=THREADS).reshape(B, H, M, D)
+    else:
+        ref = oracle_rows(host, True, scale)
+    check(out, ref, dt, f"{dt} causal pair split {case[1:6]} splits {info.key_splits}")
+
+
 def test_max_key_splits(ofh):
     """max_key_splits caps the split (1: none) and every cap gives the oracle's rows."""
     F = ofh
