@@ -496,6 +496,8 @@ int fwd_impl(const ofh_attention_params* p, const void* q, const void* k, const 
     // held until this call's launches are queued when it uses library scratch
     std::unique_lock<std::mutex> scratch_lock(g_scratch_mu, std::defer_lock);
     if (need > 0) {
+        if (ws == nullptr && noalloc)  // the allocation-free entry always passes its scratch
+            return set_error(OFH_ERROR_WORKSPACE_TOO_SMALL, "allocation-free call without its scratch");
         if (ws == nullptr) {
             scratch_lock.lock();
             // A stream under graph capture cannot allocate: a key split whose
@@ -508,8 +510,16 @@ int fwd_impl(const ofh_attention_params* p, const void* q, const void* k, const 
             if (need > 0)
                 if (int rc = library_scratch_locked(need, stream, &ws)) return rc;
         } else if (workspace_bytes < need) {
-            return set_error(OFH_ERROR_WORKSPACE_TOO_SMALL,
-                             "workspace too small: need " + std::to_string(need) + " bytes");
+            // The allocation-free entry drops a key split whose partial rows
+            // do not fit its static scratch (the split only spreads the work).
+            if (noalloc && r.key_splits > 1) {
+                no_key_split(p, r);
+                need = workspace_bytes_for(p, r);
+            }
+            if (workspace_bytes < need)
+                return set_error(OFH_ERROR_WORKSPACE_TOO_SMALL,
+                                 "workspace too small: need " + std::to_string(need) + " bytes");
+            if (need == 0) ws = nullptr;
         }
     }
     if (r.tile_list && !r.lds_list) {
@@ -616,7 +626,11 @@ int ofh_attention_fwd_noalloc(const ofh_attention_params* p, const void* q, cons
     if (int rc = validate(p, true, q, k, v, out)) return rc;
     Resolved r;
     if (int rc = resolve(p, q, k, v, out, r)) return rc;
-    const size_t need = r.algorithm == OFH_ALGO_FLASH_MFMA ? workspace_bytes_for(p, r) : 0;
+    size_t need = r.algorithm == OFH_ALGO_FLASH_MFMA ? workspace_bytes_for(p, r) : 0;
+    if (need > ofh::kNoAllocScratchBytes && r.key_splits > 1) {  // fwd_impl drops the split
+        no_key_split(p, r);
+        need = workspace_bytes_for(p, r);
+    }
     if (need > ofh::kNoAllocScratchBytes)
         return set_error(OFH_ERROR_WORKSPACE_TOO_SMALL,
                          "ofh_attention_fwd_noalloc: this call needs " + std::to_string(need) +
@@ -630,8 +644,9 @@ int ofh_attention_fwd_noalloc(const ofh_attention_params* p, const void* q, cons
     OFH_HIP_CHECK(ofh::noalloc_scratch(&ws));
     unsigned* counters = nullptr;
     OFH_HIP_CHECK(ofh::split_counter_slot(0, &counters));
-    return fwd_impl(p, q, k, v, out, need > 0 ? ws : nullptr, need > 0 ? ofh::kNoAllocScratchBytes : 0,
-                    static_cast<hipStream_t>(stream), true);
+    // The scratch is always handed over: fwd_impl plans the call again (with
+    // its key split) and drops the split there when it does not fit.
+    return fwd_impl(p, q, k, v, out, ws, ofh::kNoAllocScratchBytes, static_cast<hipStream_t>(stream), true);
 }
 
 int ofh_attention_fwd_host(const ofh_attention_params* p, const float* q, const float* k,

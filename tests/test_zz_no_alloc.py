@@ -98,3 +98,58 @@ def test_noalloc_matches_fwd(ofh):
         err, maxabs = norm_error(b, O.standard_attention(*host, prob))
         print(f"{label}: identical to ofh_attention_fwd; vs oracle normwise {err:.3e} max-abs {maxabs:.3e}")
         assert err <= TOL[dt]
+
+
+@pytest.mark.gpu
+def test_noalloc_drops_oversized_key_split(ofh):
+    """A key split whose partial rows exceed the static scratch is dropped, not
+    rejected: the call runs without the split (the split only spreads the
+    work), bit-identical to ofh_attention_fwd with max_key_splits = 1, and
+    allocates nothing (device memory unchanged across the calls)."""
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    F = ofh
+    lib = F.lib()
+    cases = [  # causal calls planned as query tile pairs with per-tile key-split ranges
+        ("bf16 causal pair split", "bf16", 1, 32, 2048, 2048, 128),
+        ("fp32 causal pair split", "f32", 2, 8, 2048, 2048, 64),
+    ]
+    stream = torch.cuda.Stream()
+    # one small call first: the entry's static arrays are looked up (and so
+    # materialised) on its first call on a device, so every call below must
+    # leave device memory exactly as it finds it
+    wq = torch.randn(1, 1, 64, 64, device="cuda").to(torch.bfloat16)
+    wo = torch.empty(1, 1, 64, 64, device="cuda", dtype=torch.float32)
+    pw = F.make_params(1, 1, 64, 64, 64, dtype=F.DTYPE_BF16, out_dtype=F.DTYPE_F32, scale=0.125)
+    F.check(lib.ofh_attention_fwd_noalloc(ctypes.byref(pw), wq.data_ptr(), wq.data_ptr(), wq.data_ptr(),
+                                          wo.data_ptr(), stream.cuda_stream))
+    stream.synchronize()
+    for i, (label, dt, B, H, M, N, D) in enumerate(cases):
+        dev, _ = make_inputs(dt, B, H, M, N, D, seed=80 + i)
+        q, k, v = dev
+        code = {"f32": F.DTYPE_F32, "bf16": F.DTYPE_BF16}[dt]
+        kw = dict(dtype=code, out_dtype=F.DTYPE_F32, scale=1.0 / math.sqrt(D), causal=True)
+        p = F.make_params(B, H, M, N, D, **kw)
+        p1 = F.make_params(B, H, M, N, D, max_key_splits=1, **kw)
+        info = F.launch_info(p)
+        need = F.workspace_bytes(p)
+        print(f"case {label}: B{B} H{H} M{M} N{N} D{D} key_splits {info.key_splits} scratch {need} bytes",
+              flush=True)
+        assert info.key_splits > 1 and need > NOALLOC_MAX, (label, info.key_splits, need)
+        assert F.workspace_bytes(p1) == 0
+        o_ref = torch.empty((B, H, M, D), device="cuda", dtype=torch.float32)
+        o_na = torch.full_like(o_ref, float("nan"))
+        torch.cuda.synchronize()
+        F.check(lib.ofh_attention_fwd(ctypes.byref(p1), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                      o_ref.data_ptr(), None, 0, stream.cuda_stream))
+        stream.synchronize()
+        free0 = torch.cuda.mem_get_info()[0]
+        for _ in range(2):
+            F.check(lib.ofh_attention_fwd_noalloc(ctypes.byref(p), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                                  o_na.data_ptr(), stream.cuda_stream))
+            stream.synchronize()
+            assert torch.cuda.mem_get_info()[0] == free0, f"{label}: device memory changed"
+        a, b = o_ref.cpu().numpy(), o_na.cpu().numpy()
+        assert np.array_equal(a, b), f"{label}: differs from the unsplit call (max {np.nanmax(np.abs(a - b))})"
+        print(f"{label}: identical to ofh_attention_fwd without a split", flush=True)
