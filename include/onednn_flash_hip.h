@@ -156,9 +156,10 @@ int ofh_attention_fwd(const ofh_attention_params* p, const void* q, const void* 
  * device memory inside the call (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). Its scratch (block-mask tile lists,
  * key-split partial rows) is a static device array of 16 MiB (16777216 bytes)
- * that every GPU the library runs on holds until the process ends; calls that
- * need more scratch than that (ofh_attention_workspace_bytes) fail with
- * OFH_ERROR_WORKSPACE_TOO_SMALL before any launch. It calls no hipMalloc or
+ * that every GPU the library runs on holds until the process ends. A key
+ * split whose partial rows do not fit is dropped (the call runs unsplit, with
+ * the same result); calls that still need more scratch than that (block-mask
+ * lists) fail with OFH_ERROR_WORKSPACE_TOO_SMALL before any launch. It calls no hipMalloc or
  * hipFree; the first call on a device looks up that device's address of the
  * array once. All calls on one GPU share the array: calls that overlap on one
  * GPU (other streams, other host threads without ordering) race on it and
