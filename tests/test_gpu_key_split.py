@@ -192,10 +192,40 @@ def test_fp32_causal_pair_split(ofh, shape, cap):
     check(out, ref, "f32", f"f32 causal pair split {shape} splits {info.key_splits}")
 
 
+@pytest.mark.parametrize("mod", ["alibi_softcap", "dense_bias"])
+def test_fp32_causal_pair_split_score_mod(ofh, mod):
+    """The fp32 pair split with a score_mod: ALiBi + soft-cap, and a shared
+    dense [M, N] bias (each query tile of a pair reads its own bias rows)."""
+    F = ofh
+    B, H, M, N, D = 1, 8, 2048, 2048, 64
+    dev, host = make_inputs("f32", B, H, M, N, D, seed=131)
+    uq, uk, uv = host
+    scale = 1.0 / math.sqrt(D)
+    kw, slopes, bias, cap = {}, None, None, 0.0
+    if mod == "alibi_softcap":
+        slopes = (2.0 ** (-8.0 * np.arange(1, H + 1) / H)).astype(np.float32)
+        kw = dict(alibi_slopes=torch.from_numpy(slopes).cuda(), softcap=30.0)
+        cap = 30.0
+    else:
+        bias = O.normal(101, (M, N), std=1.5)
+        kw = dict(bias=torch.from_numpy(bias).cuda())
+    p = F.make_params(B, H, M, N, D, dtype=DTYPE["f32"], causal=True, softcap=30.0)
+    info = F.launch_info(p)
+    print(f"f32 causal pair split {mod}: key_splits {info.key_splits} workgroups {info.workgroups}", flush=True)
+    assert info.block_m == 128 and info.key_splits >= 2 and info.workgroups == B * H * 8 * info.key_splits
+    out = fwd(F, dev, "f32", True, "f32", **kw).cpu().numpy()
+    prob = O.Problem(B, H, M, N, D, D, scale=scale, causal=True, alibi_slopes=slopes, dense_bias=bias, softcap=cap)
+    head_idx = np.repeat(np.arange(B * H, dtype=np.uint64), M)
+    rows = np.tile(np.arange(M, dtype=np.uint64), B * H)
+    ref = O.standard_attention_rows(uq, uk, uv, prob, head_idx, rows, threads=THREADS).reshape(B, H, M, D)
+    check(out, ref, "f32", f"f32 causal pair split {mod} splits {info.key_splits}")
+
+
 @pytest.mark.parametrize("case", [("bf16", 1, 32, 2048, 2048, 128, {}), ("f16", 1, 20, 2800, 2800, 64, {}),
                                   ("bf16", 1, 64, 1024, 3000, 128, {}), ("f16", 1, 20, 3000, 1000, 128, {}),
                                   ("bf16", 1, 32, 2048, 2048, 96, {}), ("bf16", 1, 16, 2048, 2048, 256, {}),
-                                  ("bf16", 1, 64, 1024, 1024, 128, {"softcap": 30.0, "alibi": True})])
+                                  ("bf16", 1, 64, 1024, 1024, 128, {"softcap": 30.0, "alibi": True}),
+                                  ("f16", 1, 64, 1024, 1024, 64, {"bias": True})])
 def test_16bit_causal_pair_split(ofh, case):
     """16-bit causal calls whose query tiles would not split by a common range
     (about one CU's worth of tiles) run flash_fwd_pair_split_kernel: query
@@ -207,7 +237,10 @@ def test_16bit_causal_pair_split(ofh, case):
     dt, B, H, M, N, D, kw = case
     kw = dict(kw)
     alibi = kw.pop("alibi", False)
-    p = F.make_params(B, H, M, N, D, dtype=DTYPE[dt], causal=True, **kw)
+    dense = kw.pop("bias", False)
+    plan_kw = {key: val for key, val in kw.items() if key != "softcap"}
+    p = F.make_params(B, H, M, N, D, dtype=DTYPE[dt], causal=True,
+                      softcap=kw.get("softcap", 30.0 if dense else 0.0), **plan_kw)
     info = F.launch_info(p)
     print(f"{case}: {info.kernel_name.decode()} block_m {info.block_m} key_splits {info.key_splits} "
           f"workgroups {info.workgroups} merge_in_launch {info.merge_in_launch}", flush=True)
@@ -217,13 +250,17 @@ def test_16bit_causal_pair_split(ofh, case):
     dev, host = make_inputs(dt, B, H, M, N, D, seed=M + N + D)
     uq, uk, uv = host
     scale = 1.0 / math.sqrt(D)
-    slopes = None
+    slopes = bias = None
     if alibi:
         slopes = (2.0 ** (-8.0 * np.arange(1, H + 1) / H)).astype(np.float32)
         kw["alibi_slopes"] = torch.from_numpy(slopes).cuda()
+    if dense:  # a shared [M, N] bias (the launch plan above is the score_mod one)
+        bias = O.normal(97, (M, N), std=1.5)
+        kw["bias"] = torch.from_numpy(bias).cuda()
     out = fwd(F, dev, dt, True, "f32", **kw).cpu().numpy()
-    if alibi or "softcap" in kw:
-        prob = O.Problem(B, H, M, N, D, D, scale=scale, causal=True, alibi_slopes=slopes, softcap=kw.get("softcap", 0.0))
+    if alibi or dense or "softcap" in kw:
+        prob = O.Problem(B, H, M, N, D, D, scale=scale, causal=True, alibi_slopes=slopes, dense_bias=bias,
+                         softcap=kw.get("softcap", 0.0))
         head_idx = np.repeat(np.arange(B * H, dtype=np.uint64), M)
         rows = np.tile(np.arange(M, dtype=np.uint64), B * H)
         ref = O.standard_attention_rows(uq, uk, uv, prob, head_idx, rows, threads=THREADS).reshape(B, H, M, D)
