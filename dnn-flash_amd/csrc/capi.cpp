@@ -48,7 +48,7 @@ struct Resolved {
     int num_q_tiles, num_k_tiles;
     int key_splits;      // workgroups per query tile, each over a range of K/V tiles
     int split_tiles;     // K/V tile steps per split
-    bool pair_split;     // fp32 causal: query tile pairs, each tile split in key_splits ranges of its own length
+    bool pair_split;     // causal: query tile pairs, each tile split in key_splits ranges of its own length
 };
 
 void contiguous_strides(int64_t out[3], const int64_t in[3], size_t H, size_t T, size_t last) {
@@ -180,7 +180,7 @@ void choose_key_splits(const ofh_attention_params* p, Resolved& r) {
     // prologue, partial rows and a wider merge) measured slower (bf16 causal
     // B1 H8 N4096 D128: 3 common ranges 0.060 ms, 4 per-tile ranges 0.065).
     const bool pair_ok = !rows32 && p->causal && !r.tile_list;
-    auto pair_split = [&]() {
+    auto plan_pair_split = [&]() {
         const int64_t pairs = bh * ((r.num_q_tiles + 1) / 2);
         const int64_t kend = std::min<int64_t>((int64_t)p->key_tokens, (int64_t)r.num_q_tiles * r.block_m);
         const int64_t max_steps = (kend + r.block_n - 1) / r.block_n;
@@ -192,7 +192,7 @@ void choose_key_splits(const ofh_attention_params* p, Resolved& r) {
         r.split_tiles = 1 << 30;
         return true;
     };
-    if (pair_ok && p->dtype == OFH_DTYPE_F32 && pair_split()) return;
+    if (pair_ok && p->dtype == OFH_DTYPE_F32 && plan_pair_split()) return;
     const int64_t wgs = bh * (r.paired ? (r.num_q_tiles + 1) / 2 : r.num_q_tiles);
     if (wgs >= slots) return;
     // tile steps of each query tile (block_n keys each)
@@ -226,7 +226,7 @@ void choose_key_splits(const ofh_attention_params* p, Resolved& r) {
     const int per = per_of(lo);
     const int splits = (max_steps + per - 1) / per;
     if (splits <= 1) {
-        if (pair_ok) pair_split();
+        if (pair_ok) plan_pair_split();
         return;
     }
     r.key_splits = splits;

@@ -68,9 +68,10 @@ struct FwdArgs {
     // num_splits == 1: one workgroup per query tile.
     int num_splits;
     int split_tiles;
-    // 1 (fp32 causal calls of the 128-row kernel): workgroups take the causal
-    // query tile pairs (nqt-1-p, p) of map_work_pair, and query tile qt's steps
-    // are cut into num_splits ranges of ceil(steps(qt) / num_splits) steps
+    // 1 (causal calls of the fp32 128-row kernel and of
+    // flash_fwd_pair_split_kernel): workgroups take the causal query tile
+    // pairs (nqt-1-p, p) of map_work_pair, and query tile qt's steps are cut
+    // into num_splits ranges of ceil(steps(qt) / num_splits) steps
     // (split_tiles unused), so every workgroup runs about the same number of
     // steps; workgroup s of a pair runs split s of both tiles.
     int pair_split;
