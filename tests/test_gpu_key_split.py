@@ -312,3 +312,36 @@ def test_graph_capture(ofh, dt):
             eager = F.attention_fwd(*dev, scale=scale, out_dtype=torch.float32)
             torch.cuda.synchronize()
             check(eager.cpu().numpy(), ref, dt, f"{dt} eager call after replay {rep}")
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_graph_capture_pair_split(ofh, dt):
+    """A causal pair-split call captured in a HIP graph: with a caller
+    workspace the split and its second-launch merge are captured and kept;
+    without one the split is dropped on the capture stream. Every replay, with
+    eager calls in between, gives the oracle's rows."""
+    F = ofh
+    B, H, M, N, D = (1, 64, 1024, 1024, 64) if dt == "bf16" else (1, 8, 2048, 2048, 64)
+    dev, host = make_inputs(dt, B, H, M, N, D, seed=37)
+    ref = oracle_rows(host, True, 1.0 / math.sqrt(D))
+    p = F.make_params(B, H, M, N, D, dtype=DTYPE[dt], out_dtype=DTYPE["f32"], causal=True)
+    info = F.launch_info(p)
+    print(f"{dt} {info.kernel_name.decode()} key_splits {info.key_splits} workgroups {info.workgroups}", flush=True)
+    nqt = -(-M // info.block_m)
+    assert info.key_splits > 1 and info.merge_in_launch == 0
+    assert info.workgroups == B * H * ((nqt + 1) // 2) * info.key_splits
+    ws = torch.empty(F.workspace_bytes(p), dtype=torch.uint8, device="cuda")
+    scale = 1.0 / math.sqrt(D)
+    for use_ws in (True, False):
+        out = torch.empty((B, H, M, D), device="cuda", dtype=torch.float32)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            F.attention_fwd(*dev, scale=scale, causal=True, out=out, workspace=ws if use_ws else None)
+        for rep in range(3):
+            out.fill_(float("nan"))
+            g.replay()
+            torch.cuda.synchronize()
+            check(out.cpu().numpy(), ref, dt, f"{dt} causal pair split graph replay {rep} workspace={use_ws}")
+            eager = F.attention_fwd(*dev, scale=scale, causal=True, out_dtype=torch.float32)
+            torch.cuda.synchronize()
+            check(eager.cpu().numpy(), ref, dt, f"{dt} causal eager call after replay {rep}")
