@@ -15,9 +15,9 @@
 #include <mutex>
 #include <string>
 #include <vector>
-#include <vector>
 
 #include "ofh_kernels.h"
+#include "stream_key.h"
 
 namespace {
 
@@ -346,10 +346,11 @@ size_t partial_rows(const ofh_attention_params* p, const Resolved& r) {
 }
 // Arrival counters of the single-launch split merge: slot 0 serves the
 // allocation-free entry point, slots 1.. one stream each (first come, first
-// served). A call that finds no free slot, or runs with OFH_SPLIT_MERGE=launch
-// in the environment, merges in a second launch instead.
+// served; keyed as the scratch buffers are, see stream_key.h). A call that
+// finds no free slot, or runs with OFH_SPLIT_MERGE=launch in the environment,
+// merges in a second launch instead.
 std::mutex g_counter_mu;
-std::map<std::pair<int, hipStream_t>, int> g_counter_slots;
+std::map<ofh::StreamKey, int> g_counter_slots;
 int g_next_counter_slot = 1;
 
 int split_counters_for(hipStream_t stream, bool noalloc, unsigned** out) {
@@ -361,10 +362,11 @@ int split_counters_for(hipStream_t stream, bool noalloc, unsigned** out) {
         int dev = 0;
         OFH_HIP_CHECK(hipGetDevice(&dev));
         std::lock_guard<std::mutex> lock(g_counter_mu);
-        auto it = g_counter_slots.find({dev, stream});
+        const ofh::StreamKey key = ofh::stream_key(dev, stream);
+        auto it = g_counter_slots.find(key);
         if (it == g_counter_slots.end()) {
             if (g_next_counter_slot >= ofh::kSplitCounterSlots) return OFH_SUCCESS;
-            it = g_counter_slots.emplace(std::make_pair(dev, stream), g_next_counter_slot++).first;
+            it = g_counter_slots.emplace(key, g_next_counter_slot++).first;
         }
         slot = it->second;
     }
@@ -390,49 +392,135 @@ size_t workspace_bytes_for(const ofh_attention_params* p, const Resolved& r) {
     return n;
 }
 
-// Library-owned scratch, used when the caller passes no workspace: one buffer
-// per (device, stream). Calls on one stream run in stream order, so they can
-// share its buffer; calls on different streams never share one. The mutex is
-// held from the lookup until the call's launches are queued (fwd_impl), so a
-// buffer is grown (its stream synchronised, then freed) only when no launch
-// that uses it can still be unqueued.
+// Library-owned scratch, used when the caller passes no workspace.
+//
+// The first kDedicatedScratchStreams streams of a device (keyed by
+// stream_key: hipStreamPerThread per host thread) get a buffer each. Calls on
+// one stream run in stream order, so they can share its buffer; calls on
+// different streams never share one. A dedicated buffer grows on demand (its
+// stream synchronised, then the old buffer freed) and lives until the process
+// ends: the footprint is, per stream, the largest need of a call on it (at
+// least 1 MiB).
+//
+// Streams beyond those share one overflow buffer per device, ordered across
+// streams by an event: a call waits (on the device, hipStreamWaitEvent) for
+// the previous call that used the buffer and records the event after its own
+// launches. Growing it waits (on the host) for that last user. So the
+// library's scratch stays bounded by kDedicatedScratchStreams + 1 buffers per
+// device however many streams a caller creates.
+//
+// A stream under graph capture never grows or frees anything: it may use its
+// dedicated buffer when that already fits, which is then marked as held by a
+// graph. A held buffer is never freed: when it must grow, a new buffer
+// replaces it and the old one stays allocated until the process ends, since
+// replays of the graph still address it. Calls that do not fit return
+// OFH_ERROR_WORKSPACE_TOO_SMALL before touching the stream (key splits are
+// dropped first, which leaves the result unchanged).
+//
+// The mutex is held from the lookup until the call's launches are queued
+// (fwd_impl), so no buffer is grown while a launch that uses it is unqueued.
+constexpr int kDedicatedScratchStreams = 16;
+
 struct DeviceScratch {
     void* ptr = nullptr;
     size_t bytes = 0;
+    bool held_by_graph = false;
+};
+struct SharedScratch {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    hipEvent_t last_use = nullptr;
+    bool recorded = false;
 };
 std::mutex g_scratch_mu;
-std::map<std::pair<int, hipStream_t>, DeviceScratch> g_scratch;
-
-// Caller holds g_scratch_mu. Bytes of the library scratch of (current device, stream).
-size_t library_scratch_bytes_locked(hipStream_t stream) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 0;
-    auto it = g_scratch.find({dev, stream});
-    return it == g_scratch.end() ? 0 : it->second.bytes;
-}
+std::map<ofh::StreamKey, DeviceScratch> g_scratch;
+std::map<int, SharedScratch> g_shared_scratch;
+std::vector<void*> g_graph_held;  // replaced buffers that captured graphs still address
 
 bool stream_capturing(hipStream_t stream) {
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
     return hipStreamIsCapturing(stream, &st) == hipSuccess && st == hipStreamCaptureStatusActive;
 }
 
-// Caller holds g_scratch_mu.
-int library_scratch_locked(size_t bytes, hipStream_t stream, void** out) {
+int dedicated_scratch_count(int dev) {
+    int n = 0;
+    for (const auto& kv : g_scratch) n += kv.first.device == dev ? 1 : 0;
+    return n;
+}
+
+// Caller holds g_scratch_mu. Bytes a call on `stream` under graph capture may
+// use without allocating: its dedicated buffer's (0 without one).
+size_t capture_scratch_bytes_locked(hipStream_t stream) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    auto it = g_scratch.find(ofh::stream_key(dev, stream));
+    return it == g_scratch.end() ? 0 : it->second.bytes;
+}
+
+// Caller holds g_scratch_mu until the call's launches are queued; when
+// *shared is set, it then calls shared_scratch_release.
+int library_scratch_locked(size_t bytes, hipStream_t stream, bool capturing, void** out,
+                           SharedScratch** shared) {
+    *shared = nullptr;
     int dev = 0;
     OFH_HIP_CHECK(hipGetDevice(&dev));
-    DeviceScratch& s = g_scratch[{dev, stream}];
-    if (s.bytes < bytes) {
-        if (s.ptr != nullptr) {
-            OFH_HIP_CHECK(hipStreamSynchronize(stream));  // earlier launches on this stream may still use it
-            OFH_HIP_CHECK(hipFree(s.ptr));
-            s.ptr = nullptr;
-            s.bytes = 0;
+    const ofh::StreamKey key = ofh::stream_key(dev, stream);
+    auto it = g_scratch.find(key);
+    if (it == g_scratch.end() && !capturing && dedicated_scratch_count(dev) < kDedicatedScratchStreams)
+        it = g_scratch.emplace(key, DeviceScratch{}).first;
+    if (it != g_scratch.end()) {
+        DeviceScratch& s = it->second;
+        if (s.bytes < bytes) {
+            if (capturing)
+                return set_error(OFH_ERROR_WORKSPACE_TOO_SMALL,
+                                 "a stream under graph capture cannot grow the library's scratch: pass a "
+                                 "workspace of " + std::to_string(bytes) + " bytes");
+            if (s.ptr != nullptr) {
+                if (s.held_by_graph) {
+                    g_graph_held.push_back(s.ptr);
+                } else {
+                    OFH_HIP_CHECK(hipStreamSynchronize(stream));  // earlier launches on this stream may still use it
+                    OFH_HIP_CHECK(hipFree(s.ptr));
+                }
+                s.ptr = nullptr;
+                s.bytes = 0;
+                s.held_by_graph = false;
+            }
+            const size_t grown = std::max(bytes, (size_t)1 << 20);
+            OFH_HIP_CHECK(hipMalloc(&s.ptr, grown));
+            s.bytes = grown;
+        }
+        if (capturing) s.held_by_graph = true;
+        *out = s.ptr;
+        return OFH_SUCCESS;
+    }
+    if (capturing)
+        return set_error(OFH_ERROR_WORKSPACE_TOO_SMALL,
+                         "a stream under graph capture has no library scratch: pass a workspace of " +
+                             std::to_string(bytes) + " bytes");
+    SharedScratch& sh = g_shared_scratch[dev];
+    if (sh.last_use == nullptr) OFH_HIP_CHECK(hipEventCreateWithFlags(&sh.last_use, hipEventDisableTiming));
+    if (sh.bytes < bytes) {
+        if (sh.ptr != nullptr) {
+            if (sh.recorded) OFH_HIP_CHECK(hipEventSynchronize(sh.last_use));  // the last user has finished
+            OFH_HIP_CHECK(hipFree(sh.ptr));
+            sh.ptr = nullptr;
+            sh.bytes = 0;
         }
         const size_t grown = std::max(bytes, (size_t)1 << 20);
-        OFH_HIP_CHECK(hipMalloc(&s.ptr, grown));
-        s.bytes = grown;
+        OFH_HIP_CHECK(hipMalloc(&sh.ptr, grown));
+        sh.bytes = grown;
     }
-    *out = s.ptr;
+    if (sh.recorded) OFH_HIP_CHECK(hipStreamWaitEvent(stream, sh.last_use, 0));
+    *shared = &sh;
+    *out = sh.ptr;
+    return OFH_SUCCESS;
+}
+
+// After the launches that use the shared overflow buffer are queued.
+int shared_scratch_release(SharedScratch* sh, hipStream_t stream) {
+    OFH_HIP_CHECK(hipEventRecord(sh->last_use, stream));
+    sh->recorded = true;
     return OFH_SUCCESS;
 }
 
@@ -493,6 +581,7 @@ int fwd_impl(const ofh_attention_params* p, const void* q, const void* k, const 
     }
     size_t need = workspace_bytes_for(p, r);
     void* ws = workspace;
+    SharedScratch* shared = nullptr;  // set when ws is the device's shared overflow buffer
     // held until this call's launches are queued when it uses library scratch
     std::unique_lock<std::mutex> scratch_lock(g_scratch_mu, std::defer_lock);
     if (need > 0) {
@@ -503,12 +592,13 @@ int fwd_impl(const ofh_attention_params* p, const void* q, const void* k, const 
             // A stream under graph capture cannot allocate: a key split whose
             // partial rows do not fit the stream's library scratch is dropped
             // (the split only spreads the work; the result is the same).
-            if (r.key_splits > 1 && library_scratch_bytes_locked(stream) < need && stream_capturing(stream)) {
+            const bool capturing = stream_capturing(stream);
+            if (capturing && r.key_splits > 1 && capture_scratch_bytes_locked(stream) < need) {
                 no_key_split(p, r);
                 need = workspace_bytes_for(p, r);
             }
             if (need > 0)
-                if (int rc = library_scratch_locked(need, stream, &ws)) return rc;
+                if (int rc = library_scratch_locked(need, stream, capturing, &ws, &shared)) return rc;
         } else if (workspace_bytes < need) {
             // The allocation-free entry drops a key split whose partial rows
             // do not fit its static scratch (the split only spreads the work).
@@ -558,6 +648,7 @@ int fwd_impl(const ofh_attention_params* p, const void* q, const void* k, const 
     OFH_HIP_CHECK(ofh::launch_flash_mfma(a, p->dtype, r.general_mod, stream));
     if (r.key_splits > 1 && a.split_counters == nullptr)
         OFH_HIP_CHECK(ofh::launch_combine_splits(a, p->dtype, stream));
+    if (shared != nullptr) return shared_scratch_release(shared, stream);
     return OFH_SUCCESS;
 }
 

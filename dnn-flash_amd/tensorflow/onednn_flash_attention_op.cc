@@ -11,8 +11,10 @@
 //       the arithmetic still runs on the GPU, with copies in and out).
 // scale is 1/sqrt(D) and the mask is top-left causal when causal = true, as in
 // the reference (:91-92). query_block_size, key_block_size, use_onednn,
-// tile_kernel and qk_tile_layout are validated as in the reference; the GPU
-// kernels choose their own tiles, so the values are otherwise advisory.
+// tile_kernel and qk_tile_layout are validated as in the reference (the
+// onednn_brgemm + strided_k refusal in Compute, as its oneDNN BRGEMM builds
+// do); the GPU kernels choose their own tiles, so the values are otherwise
+// advisory.
 //
 // Build (needs TensorFlow's headers and library, see the package Makefile's
 // tf_op target): the op library links libonednn_flash_hip.so.
@@ -97,10 +99,6 @@ public:
                         qk_tile_layout_ == "brgemm_transformed_k",
                     errors::InvalidArgument("qk_tile_layout must be 'strided_k', 'copied_transposed', or "
                                             "'brgemm_transformed_k'"));
-        OP_REQUIRES(ctx, !(use_onednn_ && tile_kernel_ == "onednn_brgemm" && qk_tile_layout_ == "strided_k"),
-                    errors::InvalidArgument("tile_kernel='onednn_brgemm' does not support "
-                                            "qk_tile_layout='strided_k'; use 'copied_transposed' or "
-                                            "'brgemm_transformed_k'"));
     }
 
 protected:
@@ -129,6 +127,13 @@ protected:
             ctx->CtxFailure(s);
             return false;
         }
+        // The reference rejects this combination in Compute, after the output
+        // is allocated, with InvalidArgument, in its builds with oneDNN BRGEMM
+        // (:102-119); the tile attributes are otherwise advisory here.
+        OP_REQUIRES_VALUE_OR_FALSE(
+            ctx, !(use_onednn_ && tile_kernel_ == "onednn_brgemm" && qk_tile_layout_ == "strided_k"),
+            errors::InvalidArgument("tile_kernel='onednn_brgemm' does not support qk_tile_layout='strided_k'; "
+                                    "use 'copied_transposed' or 'brgemm_transformed_k'"));
         ofh_attention_params_init(p);
         p->batch = (size_t)q.dim_size(0);
         p->heads = (size_t)q.dim_size(1);
@@ -179,7 +184,7 @@ public:
         Tensor ws;
         void* ws_ptr = nullptr;
         if (ws_bytes > 0) {
-            OP_REQUIRES_OK(ctx, ctx->allocate_temp(DT_UINT8, TensorShape({(int64_t)ws_bytes}), &ws));
+            OP_REQUIRES_OK(ctx, ctx->allocate_temp(tensorflow::DT_UINT8, TensorShape({(int64_t)ws_bytes}), &ws));
             ws_ptr = ws.flat<uint8_t>().data();
         }
         const int rc = ofh_attention_fwd(&p, ctx->input(0).flat<T>().data(), ctx->input(1).flat<T>().data(),

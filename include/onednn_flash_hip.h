@@ -35,7 +35,9 @@
 extern "C" {
 #endif
 
-#define OFH_ABI_VERSION 1
+/* 2: ofh_attention_params gained max_key_splits and ofh_launch_info gained
+ * merge_in_launch (both appended). */
+#define OFH_ABI_VERSION 2
 
 /* Status codes. INVALID_ARGUMENT corresponds to the reference's
  * std::invalid_argument, the others to std::runtime_error. */
@@ -127,24 +129,40 @@ void ofh_attention_params_init(ofh_attention_params* p);
 int ofh_attention_workspace_bytes(const ofh_attention_params* p, size_t* bytes);
 
 /* Attention forward on device buffers, ordered on `stream` (asynchronous).
- * workspace may be NULL: the library then uses a buffer it owns, one per
- * (device, stream), grown on demand: the first call that needs more than the
- * buffer holds synchronises that stream (hipStreamSynchronize), frees the old
- * buffer and calls hipMalloc. Such a call blocks the host, so callers that
- * must not block or allocate (HIP graph capture, framework ops with their own
- * allocator) pass a workspace of ofh_attention_workspace_bytes bytes instead.
- * On a stream under graph capture with workspace NULL, a key split that does
- * not fit the stream's buffer is dropped (same result, one workgroup per
- * query tile); block-mask tile lists still need a workspace there.
+ * workspace may be NULL: the library then uses device scratch it owns.
+ *  - The first 16 streams used on a device get a buffer each (calls passing
+ *    hipStreamPerThread are keyed by host thread, since that handle names a
+ *    different stream in every thread; every other handle, NULL included,
+ *    names one stream). A buffer grows on demand: the first call on its
+ *    stream that needs more synchronises that stream (hipStreamSynchronize),
+ *    frees the old buffer and calls hipMalloc. Each buffer is at least 1 MiB
+ *    and as large as the largest need of a call on its stream, and it lives
+ *    until the process ends.
+ *  - Further streams share one overflow buffer per device. Calls that use it
+ *    are ordered across streams on the device (each waits for the previous
+ *    user's event, hipStreamWaitEvent, and records its own), and growing it
+ *    waits on the host for its last user. The scratch stays bounded by 17
+ *    buffers per device however many streams are used.
+ * Such calls may block the host or allocate, so callers that must not
+ * (HIP graph capture, framework ops with their own allocator) pass a
+ * workspace of ofh_attention_workspace_bytes bytes instead.
+ * On a stream under graph capture with workspace NULL, nothing is allocated,
+ * freed or synchronised: a key split that does not fit the stream's buffer is
+ * dropped (same result, one workgroup per query tile), and a call that still
+ * needs scratch its stream's buffer does not hold (block-mask tile lists)
+ * fails with OFH_ERROR_WORKSPACE_TOO_SMALL before anything is queued. A
+ * buffer a captured graph uses is never freed while the process runs (a later
+ * call that needs more gets a new one), since replays still address it.
+ * Replays of a graph share that buffer with calls on the stream it was
+ * captured on, so they must not overlap each other or such calls.
  * A key split with few rows per query tile (ofh_launch_info.merge_in_launch)
  * merges its partial rows in the launch itself, counting arrivals in a
- * counter slot that the library keeps per (device, stream) for up to 63
- * streams (later streams merge in a second launch); a captured graph keeps
- * its stream's slot, so replays of one graph must not overlap each other or
- * calls on that stream.
+ * counter slot that the library keeps per stream (keyed as above) for up to
+ * 63 streams (later streams merge in a second launch); a captured graph keeps
+ * its stream's slot, with the same rule for overlapping replays.
  * Calls from several host threads are safe: a thread holds the library's lock
  * from choosing the buffer until its launches are queued, and calls on
- * different streams never share a buffer.
+ * different streams never share a buffer without device-side ordering.
  * Fully-masked query rows are written as zeros, as standard_attention leaves
  * them (attention.cpp:111-113). */
 int ofh_attention_fwd(const ofh_attention_params* p, const void* q, const void* k,

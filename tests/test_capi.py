@@ -67,7 +67,7 @@ def test_struct_layout_matches(ofh):
     ofh.lib().ofh_attention_params_init(ctypes.byref(p))
     assert p.struct_size == ctypes.sizeof(ofh.AttentionParams)
     assert p.scale == 1.0 and p.dtype == ofh.DTYPE_F32 and p.algorithm == ofh.ALGO_AUTO
-    assert ofh.lib().ofh_abi_version() == 1
+    assert ofh.lib().ofh_abi_version() == 2
 
 
 def test_qk_score_struct_layout(ofh):
@@ -370,3 +370,15 @@ def test_one_hip_runtime_when_the_library_loads_before_torch():
     out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
     assert out.returncode == 0, out.stderr
     assert out.stdout.startswith("1 "), out.stdout
+
+
+def test_stream_keys_of_library_scratch(tmp_path):
+    """The per-stream scratch and counter-slot keys (csrc/stream_key.h):
+    hipStreamPerThread is keyed per host thread, other handles (NULL included)
+    per stream. Built and run on the CPU; it makes no HIP call."""
+    exe = tmp_path / "stream_key_check"
+    subprocess.run(["g++", "-std=c++17", "-O1", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
+                    f"-I{ROOT / 'dnn-flash_amd' / 'csrc'}", "-pthread",
+                    str(ROOT / "tests" / "cpp" / "stream_key_check.cpp"), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert out.returncode == 0 and out.stdout.strip() == "ok", out.stdout + out.stderr
