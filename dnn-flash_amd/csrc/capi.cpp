@@ -49,6 +49,7 @@ struct Resolved {
     int key_splits;      // workgroups per query tile, each over a range of K/V tiles
     int split_tiles;     // K/V tile steps per split
     bool pair_split;     // causal: query tile pairs, each tile split in key_splits ranges of its own length
+    int kdim;            // head dim of the MFMA kernel: max(D, Dv) rounded up to a multiple of 32
 };
 
 void contiguous_strides(int64_t out[3], const int64_t in[3], size_t H, size_t T, size_t last) {
@@ -142,10 +143,10 @@ int validate(const ofh_attention_params* p, bool check_ptrs, const void* q, cons
 // plain-scale block-mask kernels up to D = 64), the fp32 kernels two up to
 // D = 64.
 int workgroups_per_cu(const ofh_attention_params* p, const Resolved& r) {
-    if (p->dtype == OFH_DTYPE_F32) return p->head_dim <= 64 ? 2 : 1;
+    if (p->dtype == OFH_DTYPE_F32) return r.kdim <= 64 ? 2 : 1;
     if (r.threads >= 512) return 1;
-    if (r.tile_list && !r.general_mod && p->head_dim <= 64) return 3;
-    return p->head_dim < 160 ? 2 : 1;
+    if (r.tile_list && !r.general_mod && r.kdim <= 64) return 3;
+    return r.kdim < 160 ? 2 : 1;
 }
 constexpr int64_t kComputeUnits = 256;  // MI355X
 
@@ -246,8 +247,7 @@ void no_key_split(const ofh_attention_params* p, Resolved& r) {
     r.split_tiles = 1 << 30;
     r.pair_split = false;
     if (p->dtype == OFH_DTYPE_F32 && r.block_m == ofh::kRowsF32) return;  // 32-row blocks: no pairing, no list
-    const ofh::MfmaTiles t =
-        ofh::flash_mfma_tiles(p->dtype, (int)p->head_dim, r.general_mod, r.tile_list, p->causal != 0);
+    const ofh::MfmaTiles t = ofh::flash_mfma_tiles(p->dtype, r.kdim, r.general_mod, r.tile_list, p->causal != 0);
     r.paired = t.paired;
     r.block_n = t.block_n;
     r.num_k_tiles = (int)((p->key_tokens + r.block_n - 1) / r.block_n);
@@ -269,8 +269,12 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
             if (((s[i] * (int64_t)esz) & 15) != 0) return false;
         return true;
     };
-    const bool mfma_ok = p->head_dim == p->value_dim && p->head_dim <= 256 &&
-                         ofh::flash_mfma_head_dim(p->dtype, (int)p->head_dim) &&
+    // Head dims that are not the kernel's own (not a multiple of 32, or D != Dv)
+    // run on the kernel of max(D, Dv) rounded up to a multiple of 32.
+    r.kdim = p->head_dim <= 256 && p->value_dim <= 256
+                 ? ofh::flash_mfma_kernel_dim(p->dtype, (int)p->head_dim, (int)p->value_dim)
+                 : 0;
+    const bool mfma_ok = r.kdim > 0 &&
                          (p->dtype != OFH_DTYPE_F32 || p->out_dtype == OFH_DTYPE_F32) &&
                          aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) &&
                          strides_ok(r.qs, es) && strides_ok(r.ks, es) && strides_ok(r.vs, es) &&
@@ -279,8 +283,8 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
                          std::llabs((long long)r.ks[2]) <= (1 << 24) && std::llabs((long long)r.vs[2]) <= (1 << 24);
     if (p->algorithm == OFH_ALGO_FLASH_MFMA && !mfma_ok)
         return set_error(OFH_ERROR_UNSUPPORTED,
-                         "flash MFMA kernel needs head_dim == value_dim in {32, 64, 96, 128} (fp32) or a "
-                         "multiple of 32 up to 256 (bf16/fp16), 16-byte "
+                         "flash MFMA kernel needs head_dim and value_dim multiples of 4 up to 128 (fp32) "
+                         "or of 8 up to 256 (bf16/fp16), 16-byte "
                          "aligned rows and K/V token strides of at most 2^24 elements; use "
                          "OFH_ALGO_AUTO or OFH_ALGO_ROWWISE");
     if (p->algorithm == OFH_ALGO_ROWWISE || !mfma_ok) {
@@ -302,8 +306,7 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
     }
     r.algorithm = OFH_ALGO_FLASH_MFMA;
     const ofh::MfmaTiles tiles =
-        ofh::flash_mfma_tiles(p->dtype, (int)p->head_dim, r.general_mod, p->mask_allowed != nullptr,
-                              p->causal != 0);
+        ofh::flash_mfma_tiles(p->dtype, r.kdim, r.general_mod, p->mask_allowed != nullptr, p->causal != 0);
     r.block_m = tiles.block_m;
     r.block_n = tiles.block_n;
     r.threads = tiles.threads;
@@ -858,8 +861,8 @@ int ofh_attention_launch_info(const ofh_attention_params* p, ofh_launch_info* in
         info->key_splits = r.key_splits;
         info->merge_in_launch = merge_in_launch(p, r) ? 1 : 0;
         name = (p->dtype == OFH_DTYPE_F32 && r.block_m == ofh::kRowsF32)
-                   ? rows32_kernel_name((int)p->head_dim, r.general_mod)
-                   : ofh::flash_mfma_kernel_name(p->dtype, (int)p->head_dim, r.general_mod, r.tile_list);
+                   ? rows32_kernel_name(r.kdim, r.general_mod)
+                   : ofh::flash_mfma_kernel_name(p->dtype, r.kdim, r.general_mod, r.tile_list);
         // 16-bit causal pairs with a key split run the same tiling in a kernel of their own
         static thread_local std::string pair_name;
         const std::string lockstep = "flash_fwd_lockstep_kernel";

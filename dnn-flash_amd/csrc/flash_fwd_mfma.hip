@@ -28,6 +28,7 @@
 // next MFMA wants in a lane (k-slots 8g..8g+7 of a 16-wide chunk), and what
 // a 16-byte store of the output wants.
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <string>
@@ -624,9 +625,14 @@ struct Wave32 {
         my_q = qw0 + r;
         // Q^T fragments (B operand of S^T = K Q^T): lane holds Q[my_q][16c + 8g .. +7].
         // Rows past the end read the last row; their results are never stored.
+        // Columns at or past a.D (the kernel's D is the head dim rounded up) are zero.
         const T* qrow = Qp + (int64_t)min(my_q, a.M - 1) * a.q_sm + 8 * g;
 #pragma unroll
-        for (int c = 0; c < D / 16; ++c) qf[c] = __builtin_bit_cast(v8, *(const u32x4*)(qrow + 16 * c));
+        for (int c = 0; c < D / 16; ++c) {
+            u32x4 u = {0u, 0u, 0u, 0u};
+            if (16 * c + 8 * g < a.D) u = *(const u32x4*)(qrow + 16 * c);
+            qf[c] = __builtin_bit_cast(v8, u);
+        }
 #pragma unroll
         for (int db = 0; db < D / 32; ++db) o[db] = f32x16{};
         m_run = kNegInf;
@@ -663,9 +669,16 @@ struct Wave32 {
         const int slot0 = 64 * wave + lane;
         dma_row0 = slot0 / L::CPR;
         const int pos = slot0 % L::CPR;
-        dma_koff = dma_row0 * (int)a.k_sn + 8 * (pos ^ L::kswz(dma_row0));
-        dma_voff = dma_row0 * (int)a.v_sn + 8 * (pos ^ L::vswz(dma_row0));
+        dma_koff = dma_row0 * (int)a.k_sn + 8 * src_chunk(pos ^ L::kswz(dma_row0), a.D);
+        dma_voff = dma_row0 * (int)a.v_sn + 8 * src_chunk(pos ^ L::vswz(dma_row0), a.Dv);
     }
+
+    // Source chunk of the 16-byte chunk c of a K/V row whose real width is
+    // `width` elements (the kernel's D may round the head dims up): chunks at
+    // or past the real width repeat the row's last real chunk, finite data
+    // that meets the zero Q columns (K) or fills O^T rows that are never
+    // stored (V).
+    static __device__ __forceinline__ int src_chunk(int c, int width) { return min(c, (width >> 3) - 1); }
 
     // Entry of tile step `it` (a global load with a list: issue it early).
     __device__ __forceinline__ int entry(int it) const { return LIST ? list[it] : it; }
@@ -694,8 +707,9 @@ struct Wave32 {
                 const int slot = 64 * (u * NW + wave) + (tid & 63);
                 const int row = slot / L::CPR, pos = slot - row * L::CPR;
                 const int rr = min(k0 + row, a.N - 1) - k0;
-                dma16(kt_base + (int64_t)rr * a.k_sn + 8 * (pos ^ L::kswz(row)), lds0 + 1024 * NW * u);
-                dma16(vt_base + (int64_t)rr * a.v_sn + 8 * (pos ^ L::vswz(row)), lds0 + L::KTILE + 1024 * NW * u);
+                dma16(kt_base + (int64_t)rr * a.k_sn + 8 * src_chunk(pos ^ L::kswz(row), a.D), lds0 + 1024 * NW * u);
+                dma16(vt_base + (int64_t)rr * a.v_sn + 8 * src_chunk(pos ^ L::vswz(row), a.Dv),
+                      lds0 + L::KTILE + 1024 * NW * u);
             }
             return;
         }
@@ -1006,12 +1020,13 @@ struct Wave32 {
         const float l_tot = l_run + __shfl_xor(l_run, 32);
         if (my_q >= a.M) return;
         const int64_t prow = ((int64_t)split * a.B * a.H + (int64_t)b * a.H + h) * a.M + my_q;
-        float* po = a.part_o + prow * D + 8 * g;
+        float* po = a.part_o + prow * a.Dv + 8 * g;
         const bool coh = a.split_counters != nullptr;
 #pragma unroll
         for (int db = 0; db < D / 32; ++db) {
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
+                if (32 * db + 16 * cc + 8 * g >= a.Dv) continue;  // past the value dim
                 f32x4 lo, hi;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
@@ -1039,6 +1054,7 @@ struct Wave32 {
             for (int db = 0; db < D / 32; ++db) {
 #pragma unroll
                 for (int cc = 0; cc < 2; ++cc) {
+                    if (32 * db + 16 * cc + 8 * g >= a.Dv) continue;  // past the value dim
                     f32x4 lo, hi;
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
@@ -1055,6 +1071,7 @@ struct Wave32 {
             for (int db = 0; db < D / 32; ++db) {
 #pragma unroll
                 for (int cc = 0; cc < 2; ++cc) {
+                    if (32 * db + 16 * cc + 8 * g >= a.Dv) continue;  // past the value dim
                     v8 val;
 #pragma unroll
                     for (int t = 0; t < 8; ++t) val[t] = (T)(o[db][8 * cc + t] * inv);
@@ -1442,13 +1459,15 @@ __device__ __forceinline__ void mfma32_qtile(const FwdArgs& a, float* lds, int b
     const int qw0 = q0 + wave * kQueriesPerWave;
     const int my_q = qw0 + r;
 
+    // Q^T operand: lane holds Q[my_q][g*D/2 + s]; rows past M and columns at
+    // or past a.D (the kernel's D is the head dim rounded up) are zero
     float qf[D / 2];
     {
         const float* qrow = Qp + (int64_t)my_q * a.q_sm + g * (D / 2);
 #pragma unroll
         for (int c = 0; c < D / 8; ++c) {
             f32x4 u = {0.f, 0.f, 0.f, 0.f};
-            if (my_q < a.M) u = *(const f32x4*)(qrow + 4 * c);
+            if (my_q < a.M && g * (D / 2) + 4 * c < a.D) u = *(const f32x4*)(qrow + 4 * c);
 #pragma unroll
             for (int t = 0; t < 4; ++t) qf[4 * c + t] = u[t];
         }
@@ -1480,10 +1499,9 @@ __device__ __forceinline__ void mfma32_qtile(const FwdArgs& a, float* lds, int b
             const int kj = k0 + row;
             kreg[u] = f32x4{0.f, 0.f, 0.f, 0.f};
             vreg[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (kj < a.N) {
-                kreg[u] = *(const f32x4*)(Kp + (int64_t)kj * a.k_sn + 4 * cc);
-                vreg[u] = *(const f32x4*)(Vp + (int64_t)kj * a.v_sn + 4 * cc);
-            }
+            // columns past the head dims stay zero
+            if (kj < a.N && 4 * cc < a.D) kreg[u] = *(const f32x4*)(Kp + (int64_t)kj * a.k_sn + 4 * cc);
+            if (kj < a.N && 4 * cc < a.Dv) vreg[u] = *(const f32x4*)(Vp + (int64_t)kj * a.v_sn + 4 * cc);
         }
     };
     auto store_tile = [&](int buf) {
@@ -1576,12 +1594,13 @@ __device__ __forceinline__ void mfma32_qtile(const FwdArgs& a, float* lds, int b
         // partial row: unnormalised O and (m, l), merged by the last split to arrive
         if (my_q < a.M) {
             const int64_t prow = ((int64_t)split * a.B * a.H + bh) * a.M + my_q;
-            float* po = a.part_o + prow * D + 4 * g;
+            float* po = a.part_o + prow * a.Dv + 4 * g;
             const bool coh = a.split_counters != nullptr;
 #pragma unroll
             for (int db = 0; db < D / 32; ++db) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
+                    if (32 * db + 8 * i + 4 * g >= a.Dv) continue;  // past the value dim
                     f32x4 val;
 #pragma unroll
                     for (int j = 0; j < 4; ++j) val[j] = o[db][4 * i + j];
@@ -1608,6 +1627,7 @@ __device__ __forceinline__ void mfma32_qtile(const FwdArgs& a, float* lds, int b
         for (int db = 0; db < D / 32; ++db) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
+                if (32 * db + 8 * i + 4 * g >= a.Dv) continue;  // past the value dim
                 f32x4 val;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) val[j] = o[db][4 * i + j] * inv;
@@ -1681,7 +1701,9 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_f32_rows32_kernel(FwdArg
         const float* qrow = Qp + (int64_t)min(my_q, a.M - 1) * a.q_sm + g * (D / 2);
 #pragma unroll
         for (int c = 0; c < D / 8; ++c) {
-            f32x4 u = *(const f32x4*)(qrow + 4 * c);
+            f32x4 u = {0.f, 0.f, 0.f, 0.f};
+            // columns at or past a.D (the kernel's D rounds the head dim up) are zero
+            if (g * (D / 2) + 4 * c < a.D) u = *(const f32x4*)(qrow + 4 * c);
             if (my_q >= a.M) u = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int t = 0; t < 4; ++t) qf[4 * c + t] = u[t];
@@ -1710,14 +1732,18 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_f32_rows32_kernel(FwdArg
         const int k0 = it * kBlockNF32;
         const float* krow = Kp + (int64_t)min(k0 + kappa(r), a.N - 1) * a.k_sn + g * (D / 2);
 #pragma unroll
-        for (int c = 0; c < D / 8; ++c) t.k[c] = *(const f32x4*)(krow + 4 * c);
+        for (int c = 0; c < D / 8; ++c) {
+            t.k[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (g * (D / 2) + 4 * c < a.D) t.k[c] = *(const f32x4*)(krow + 4 * c);
+        }
 #pragma unroll
         for (int u = 0; u < 16; ++u) {
             const int kj = k0 + acc_pos(u, g);
             const float* vrow = Vp + (int64_t)min(kj, a.N - 1) * a.v_sn + r;
 #pragma unroll
             for (int db = 0; db < D / 32; ++db) {
-                const float x = vrow[32 * db];
+                float x = 0.0f;
+                if (r + 32 * db < a.Dv) x = vrow[32 * db];
                 t.v[u][db] = kj < a.N ? x : 0.0f;
             }
         }
@@ -1794,11 +1820,12 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_f32_rows32_kernel(FwdArg
         const bool coh = a.split_counters != nullptr;
         if (wave == 0 && my_q < a.M) {
             const int64_t prow = ((int64_t)split * a.B * a.H + bh) * a.M + my_q;
-            float* po = a.part_o + prow * D + 4 * g;
+            float* po = a.part_o + prow * a.Dv + 4 * g;
 #pragma unroll
             for (int db = 0; db < D / 32; ++db) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
+                    if (32 * db + 8 * i + 4 * g >= a.Dv) continue;  // past the value dim
                     f32x4 val;
 #pragma unroll
                     for (int j = 0; j < 4; ++j) val[j] = o[db][4 * i + j];
@@ -1824,6 +1851,7 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_f32_rows32_kernel(FwdArg
         for (int db = 0; db < D / 32; ++db) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
+                if (32 * db + 8 * i + 4 * g >= a.Dv) continue;  // past the value dim
                 f32x4 val;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) val[j] = o[db][4 * i + j] * inv;
@@ -1978,9 +2006,12 @@ static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
 }
 
 hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipStream_t s) {
+    // the kernel's head dim: D and Dv rounded up (the kernels zero-pad Q and
+    // mask the stores past Dv)
+    const int kd = flash_mfma_kernel_dim(dtype, a.D, a.Dv);
     if (dtype == DT_BF16 || dtype == DT_F16) {
         const bool f16 = dtype == DT_F16;
-        switch (a.D) {
+        switch (kd) {
             case 32: return f16 ? launch16<_Float16, 32>(a, general_mod, s) : launch16<__bf16, 32>(a, general_mod, s);
             case 64: return f16 ? launch16<_Float16, 64>(a, general_mod, s) : launch16<__bf16, 64>(a, general_mod, s);
             case 96: return f16 ? launch16<_Float16, 96>(a, general_mod, s) : launch16<__bf16, 96>(a, general_mod, s);
@@ -1994,7 +2025,7 @@ hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipS
     } else if (dtype == DT_F32) {
         if (a.split_bm == kRowsF32) {  // few query rows: 32-row blocks (no block mask)
             if (a.tile_counts != nullptr) return hipErrorInvalidValue;
-            switch (a.D) {
+            switch (kd) {
                 case 32: return general_mod ? launch(flash_fwd_f32_rows32_kernel<32, true>, kThreads32, a, s)
                                             : launch(flash_fwd_f32_rows32_kernel<32, false>, kThreads32, a, s);
                 case 64: return general_mod ? launch(flash_fwd_f32_rows32_kernel<64, true>, kThreads32, a, s)
@@ -2006,16 +2037,16 @@ hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipS
                 default: return hipErrorInvalidValue;
             }
         }
-        if (a.D == 96)
+        if (kd == 96)
             return general_mod ? launch(flash_fwd_mfma32_kernel<96, true, kTilesF32>, kThreads32, a, s, a.pair_split != 0)
                                : launch(flash_fwd_mfma32_kernel<96, false, kTilesF32>, kThreads32, a, s, a.pair_split != 0);
-        if (a.D == 32)
+        if (kd == 32)
             return general_mod ? launch(flash_fwd_mfma32_kernel<32, true, kTilesF32>, kThreads32, a, s, a.pair_split != 0)
                                : launch(flash_fwd_mfma32_kernel<32, false, kTilesF32>, kThreads32, a, s, a.pair_split != 0);
-        if (a.D == 64)
+        if (kd == 64)
             return general_mod ? launch(flash_fwd_mfma32_kernel<64, true, kTilesF32>, kThreads32, a, s, a.pair_split != 0)
                                : launch(flash_fwd_mfma32_kernel<64, false, kTilesF32>, kThreads32, a, s, a.pair_split != 0);
-        if (a.D == 128)
+        if (kd == 128)
             return general_mod ? launch(flash_fwd_mfma32_kernel<128, true, kTilesF32>, kThreads32, a, s, a.pair_split != 0)
                                : launch(flash_fwd_mfma32_kernel<128, false, kTilesF32>, kThreads32, a, s, a.pair_split != 0);
     }
@@ -2071,6 +2102,13 @@ hipError_t split_counter_slot(int slot, unsigned** ptr) {
 bool flash_mfma_head_dim(int dtype, int D) {
     if (dtype == DT_F32) return D == 32 || D == 64 || D == 96 || D == 128;
     return D % 32 == 0 && D >= 32 && D <= 256;
+}
+
+int flash_mfma_kernel_dim(int dtype, int D, int Dv) {
+    const int unit = dtype == DT_F32 ? 4 : 8;  // elements per 16-byte row chunk
+    if (D <= 0 || Dv <= 0 || D % unit != 0 || Dv % unit != 0) return 0;
+    const int kd = (std::max(D, Dv) + 31) / 32 * 32;
+    return flash_mfma_head_dim(dtype, kd) ? kd : 0;
 }
 
 const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile_list) {

@@ -15,7 +15,8 @@
 //   flash_attention_q_tile (tile 0), flash_attention_qk_pv_tile (tile 0),
 //   flash_attention_qk_pv_tile_ws for every tile, flash_attention_batched_qk_pv_tile
 //   (one head), run_attention(StandardReference), run_attention(FlashTiledReference),
-//   and, when the case has an ALiBi slope, flash_attention_tiled with the slope
+//   run_attention(FlashMfmaHip) (the MFMA kernel, also for head dims that are not
+//   a multiple of 32 and D != Dv), and, when the case has an ALiBi slope, flash_attention_tiled with the slope
 //   as per-head alibi_slopes instead of the ScoreBiasFn.
 // Exit code 0 when every call returned; the values are judged by the caller.
 
@@ -106,6 +107,8 @@ int main(int argc, char** argv) {
         outs.push_back(bout);
         outs.push_back(of::run_attention(of::AttentionBackendKind::StandardReference, q, k, v, shape, opt));
         outs.push_back(of::run_attention(of::AttentionBackendKind::FlashTiledReference, q, k, v, shape, opt));
+        // demands the MFMA kernel (throws where none serves the head dims)
+        outs.push_back(of::run_attention(of::AttentionBackendKind::FlashMfmaHip, q, k, v, shape, opt));
         if (has_alibi) {
             of::AttentionOptions o = opt;
             o.score_bias = nullptr;

@@ -307,8 +307,9 @@ int main() {
         of::standard_attention(q, k, v, shape, o);
     }, "bad BlockMask throws invalid_argument");
     expect_throw<std::runtime_error>([&] {
-        of::run_attention(of::AttentionBackendKind::FlashMfmaHip, sin_values(128 * 80, 0.f), sin_values(128 * 80, 1.f),
-                          sin_values(128 * 80, 2.f), of::AttentionShape{128, 128, 80, 80}, options);
+        // fp32 MFMA kernels serve head dims up to 128
+        of::run_attention(of::AttentionBackendKind::FlashMfmaHip, sin_values(128 * 160, 0.f), sin_values(128 * 160, 1.f),
+                          sin_values(128 * 160, 2.f), of::AttentionShape{128, 128, 160, 160}, options);
     }, "unsupported MFMA shape throws runtime_error");
 
     std::printf("%s\n", failures == 0 ? "ALL OK" : "FAILURES");

@@ -149,7 +149,9 @@ def test_validation_messages(ofh):
                   "softcap")
     _expect_error(F, F.make_params(1, 1, 4, 4, 64, bias_kind=F.BIAS_ALIBI),
                   F.OFH_ERROR_INVALID_ARGUMENT, "slopes")
-    _expect_error(F, F.make_params(1, 1, 4, 4, 80, algorithm=F.ALGO_FLASH_MFMA),
+    _expect_error(F, F.make_params(1, 1, 4, 4, 20, dtype=F.DTYPE_BF16, algorithm=F.ALGO_FLASH_MFMA),
+                  F.OFH_ERROR_UNSUPPORTED, "flash MFMA kernel needs")
+    _expect_error(F, F.make_params(1, 1, 4, 4, 160, algorithm=F.ALGO_FLASH_MFMA),
                   F.OFH_ERROR_UNSUPPORTED, "flash MFMA kernel needs")
     _expect_error(F, F.make_params(1, 1, 4, 4, 64, max_key_splits=-1), F.OFH_ERROR_INVALID_ARGUMENT,
                   "max_key_splits")
@@ -194,8 +196,18 @@ def test_kernel_choice(ofh):
         (dict(dtype=F.DTYPE_BF16, head_dim=96), "flash_fwd_lockstep_kernel<bf16,96,plain,8w,2x64keys>"),
         (dict(dtype=F.DTYPE_F16, head_dim=160, softcap=5.0), "flash_fwd_lockstep_kernel<f16,160,mod,8w,2x64keys>"),
         (dict(dtype=F.DTYPE_BF16, head_dim=192), "flash_fwd_lockstep_kernel<bf16,192,plain,4w>"),
-        (dict(dtype=F.DTYPE_BF16, head_dim=80), "rowwise_fwd_kernel"),
-        (dict(dtype=F.DTYPE_BF16, head_dim=64, value_dim=128), "rowwise_fwd_kernel"),
+        # head dims that are not a kernel's own: the kernel of max(D, Dv) rounded up to 32
+        (dict(dtype=F.DTYPE_BF16, head_dim=80), "flash_fwd_lockstep_kernel<bf16,96,plain,8w,2x64keys>"),
+        (dict(dtype=F.DTYPE_BF16, head_dim=64, value_dim=128), "flash_fwd_lockstep_kernel<bf16,128,plain,8w,2x64keys>"),
+        (dict(dtype=F.DTYPE_F16, head_dim=16), "flash_fwd_lockstep_kernel<f16,32,plain,8w,128keys>"),
+        (dict(dtype=F.DTYPE_BF16, head_dim=192, value_dim=128, softcap=5.0), "flash_fwd_lockstep_kernel<bf16,192,mod,4w>"),
+        (dict(dtype=F.DTYPE_F32, head_dim=64, value_dim=48), "flash_fwd_f32_rows32_kernel<64,plain>"),
+        (dict(dtype=F.DTYPE_F32, head_dim=40, shape=(8, 16, 1024, 300)), "flash_fwd_mfma32_kernel<64,plain>"),
+        # not a multiple of the 16-byte row chunk, or beyond the kernels' head dims: rowwise
+        (dict(dtype=F.DTYPE_BF16, head_dim=20), "rowwise_fwd_kernel"),
+        (dict(dtype=F.DTYPE_F32, head_dim=6), "rowwise_fwd_kernel"),
+        (dict(dtype=F.DTYPE_BF16, head_dim=264), "rowwise_fwd_kernel"),
+        (dict(dtype=F.DTYPE_F32, head_dim=64, value_dim=160), "rowwise_fwd_kernel"),
         (dict(dtype=F.DTYPE_F32, head_dim=64, algorithm=F.ALGO_ROWWISE), "rowwise_fwd_kernel"),
     ]
     for kw, name in cases:

@@ -81,10 +81,10 @@ def test_cpp_api_against_compiled_reference(case, tmp_path):
     names = ["standard_attention", "flash_attention_tiled", "flash_attention_q_tile",
              "flash_attention_qk_pv_tile"] + [f"flash_attention_qk_pv_tile_ws{tuple(t)}" for t in z["tiles"]] + \
             ["flash_attention_batched_qk_pv_tile", "run_attention(StandardReference)",
-             "run_attention(FlashTiledReference)"]
+             "run_attention(FlashTiledReference)", "run_attention(FlashMfmaHip)"]
     expected = [std, z["tiled"] if "tiled" in z.files else std,
                 z["q_tile"] if "q_tile" in z.files else std,
-                z["qk_pv_tile"] if "qk_pv_tile" in z.files else std] + list(z["flash_ws"]) + [std, std, std]
+                z["qk_pv_tile"] if "qk_pv_tile" in z.files else std] + list(z["flash_ws"]) + [std, std, std, std]
     if "alibi_slope" in z.files:
         names.append("flash_attention_tiled(alibi_slopes)")
         expected.append(std)
