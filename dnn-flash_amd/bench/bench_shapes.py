@@ -9,8 +9,10 @@ microseconds per call (the whole call: every launch it makes), useful TFLOP/s
 peak, and the algorithmic HBM rate (Q, K, V read once, O written once) against
 8 TB/s, with the kernel choice of ofh_attention_launch_info.
 
-    python dnn-flash_amd/bench/bench_shapes.py --shape 1,8,1,32768,128 --dtype bf16 \
+    python dnn-flash_amd/bench/bench_shapes.py --shape 1,8,1,32768,128[,Dv] --dtype bf16 \
         [--causal] [--max-key-splits S] [--algorithm auto|mfma|rowwise] [--steps K] [--warmup W]
+
+(Dv defaults to D.)
 """
 
 from __future__ import annotations
@@ -29,7 +31,7 @@ PEAK_GBS = 8000.0
 
 def main() -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--shape", action="append", required=True, help="B,H,M,N,D")
+    ap.add_argument("--shape", action="append", required=True, help="B,H,M,N,D[,Dv]")
     ap.add_argument("--dtype", default="bf16", choices=["bf16", "f16", "f32"])
     ap.add_argument("--out-dtype", default="f32", choices=["bf16", "f16", "f32"])
     ap.add_argument("--causal", action="store_true")
@@ -45,14 +47,16 @@ def main() -> int:
     tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
     code = {"f32": F.DTYPE_F32, "bf16": F.DTYPE_BF16, "f16": F.DTYPE_F16}
     for spec in args.shape:
-        B, H, M, N, D = (int(x) for x in spec.split(","))
+        dims = [int(x) for x in spec.split(",")]
+        B, H, M, N, D = dims[:5]
+        Dv = dims[5] if len(dims) > 5 else D
         g = torch.Generator(device="cuda").manual_seed(1)
         q = torch.randn((B, H, M, D), device="cuda", generator=g).to(tdt[args.dtype])
         k = torch.randn((B, H, N, D), device="cuda", generator=g).to(tdt[args.dtype])
-        v = torch.randn((B, H, N, D), device="cuda", generator=g).to(tdt[args.dtype])
-        out = torch.empty((B, H, M, D), device="cuda", dtype=tdt[args.out_dtype])
+        v = torch.randn((B, H, N, Dv), device="cuda", generator=g).to(tdt[args.dtype])
+        out = torch.empty((B, H, M, Dv), device="cuda", dtype=tdt[args.out_dtype])
         algo = {"auto": F.ALGO_AUTO, "mfma": F.ALGO_FLASH_MFMA, "rowwise": F.ALGO_ROWWISE}[args.algorithm]
-        p = F.make_params(B, H, M, N, D, dtype=code[args.dtype], out_dtype=code[args.out_dtype],
+        p = F.make_params(B, H, M, N, D, Dv, dtype=code[args.dtype], out_dtype=code[args.out_dtype],
                           causal=args.causal, max_key_splits=args.max_key_splits, algorithm=algo)
         info = F.launch_info(p)
         flops = F.useful_flops(p)
@@ -79,7 +83,7 @@ def main() -> int:
         tf = flops / us / 1e6
         gbs = hbm / us / 1e3
         print(json.dumps({
-            "shape": {"B": B, "H": H, "M": M, "N": N, "D": D}, "dtype": args.dtype,
+            "shape": {"B": B, "H": H, "M": M, "N": N, "D": D, "Dv": Dv}, "dtype": args.dtype,
             "out_dtype": args.out_dtype, "causal": bool(args.causal),
             "kernel": info.kernel_name.decode(), "key_splits": info.key_splits,
             "workgroups": info.workgroups, "us_per_call": round(us, 2),
