@@ -4,9 +4,11 @@
 A step is one attention forward call (the HIP kernels behind the C ABI) over
 one batch of synthetic device-resident inputs. Default workload: bf16 causal
 attention, B=4 H=32 N=4096 D=128 (the headline configuration). Prints ONE JSON
-line with the useful-FLOP throughput, the roofline figures of the attention
-kernel (per-launch durations measured with HIP events on the launch stream)
-and a CPU baseline: the reference's own CPU flash path (compiled from its
+line with the useful-FLOP throughput (K steps back to back between two HIP
+events on the launch stream), the roofline figures of the attention kernel
+(the same events: the mean launch duration, launch gaps included; the spread
+of single launches from a second pass with an event per launch) and a CPU
+baseline: the reference's own CPU flash path (compiled from its
 sources into oracle/_ref) on a bounded sample of the same workload, run on the
 host cores (the oracle's restatement when oracle/_ref is absent).
 
@@ -230,19 +232,31 @@ def main() -> int:
         step()
     torch.cuda.synchronize()
 
-    # timed region: K steps, an event before every launch and after the last one
-    events = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    # timed region: K steps back to back between two events on the launch
+    # stream; the mean launch duration is the region over K (launch gaps
+    # included, so it bounds the kernel time from above)
+    e_start, e_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    e_start.record(stream)
+    for _ in range(args.steps):
+        step()
+    e_end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e_start.elapsed_time(e_end) / args.steps
+    avg_launch_ms = ms
+
+    # spread of single launches: a second pass of K steps (not timed for the
+    # value) with an event before every launch and after the last one, which
+    # adds a few microseconds of device time per step
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     for i in range(args.steps):
         events[i].record(stream)
         step()
     events[-1].record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
     per_launch = [events[i].elapsed_time(events[i + 1]) for i in range(args.steps)]
-    ms = events[0].elapsed_time(events[-1]) / args.steps
-    avg_launch_ms = sum(per_launch) / len(per_launch)
     srt = sorted(per_launch)
 
     def pct(p):  # nearest-rank percentile
@@ -275,7 +289,7 @@ def main() -> int:
             "useful_gflop": round(flops / 1e9, 3),
         },
         "pct_bf16_peak": round(100.0 * value / C.PEAK_TFLOPS["bf16"], 2),
-        "launch_ms": {"mean": round(avg_launch_ms, 5), "median": round(pct(0.5), 5),
+        "launch_ms": {"mean": round(sum(per_launch) / len(per_launch), 5), "median": round(pct(0.5), 5),
                       "p10": round(pct(0.1), 5), "p90": round(pct(0.9), 5),
                       "min": round(srt[0], 5), "max": round(srt[-1], 5)},
         "wall_s_timed": round(wall, 4),
