@@ -64,10 +64,11 @@ typedef enum ofh_bias_kind {
 } ofh_bias_kind;
 
 /* Which kernel family runs. AUTO picks the MFMA flash kernel when the shape
- * is supported (D == Dv in {32, 64, 96, 128} for fp32, a multiple of 32 up to 256 for bf16/fp16;
- * 16-byte aligned rows) and the rowwise
- * kernel otherwise. ROWWISE is the exact two-pass softmax of
- * standard_attention, run on the GPU one query row per wavefront. */
+ * is supported (head_dim and value_dim multiples of 4 up to 128 for fp32, of
+ * 8 up to 256 for bf16/fp16, D != Dv allowed: the kernel of max(D, Dv)
+ * rounded up to 32 runs with the padding zeroed in place; 16-byte aligned
+ * rows) and the rowwise kernel otherwise. ROWWISE is the exact two-pass
+ * softmax of standard_attention, run on the GPU one query row per wavefront. */
 typedef enum ofh_algorithm {
     OFH_ALGO_AUTO = 0,
     OFH_ALGO_FLASH_MFMA = 1,
