@@ -587,6 +587,16 @@ int fwd_impl(const ofh_attention_params* p, const void* q, const void* k, const 
     SharedScratch* shared = nullptr;  // set when ws is the device's shared overflow buffer
     // held until this call's launches are queued when it uses library scratch
     std::unique_lock<std::mutex> scratch_lock(g_scratch_mu, std::defer_lock);
+    // Once this call holds the shared buffer, its event is recorded on every
+    // way out (also after a failed launch, whose earlier launches may use the
+    // buffer), before the lock is released: the next user waits for them.
+    struct SharedRelease {
+        SharedScratch** sh;
+        hipStream_t stream;
+        ~SharedRelease() {  // an error path: the call's own error message stays
+            if (*sh != nullptr && hipEventRecord((*sh)->last_use, stream) == hipSuccess) (*sh)->recorded = true;
+        }
+    } shared_release{&shared, stream};
     if (need > 0) {
         if (ws == nullptr && noalloc)  // the allocation-free entry always passes its scratch
             return set_error(OFH_ERROR_WORKSPACE_TOO_SMALL, "allocation-free call without its scratch");
@@ -651,7 +661,11 @@ int fwd_impl(const ofh_attention_params* p, const void* q, const void* k, const 
     OFH_HIP_CHECK(ofh::launch_flash_mfma(a, p->dtype, r.general_mod, stream));
     if (r.key_splits > 1 && a.split_counters == nullptr)
         OFH_HIP_CHECK(ofh::launch_combine_splits(a, p->dtype, stream));
-    if (shared != nullptr) return shared_scratch_release(shared, stream);
+    if (shared != nullptr) {
+        SharedScratch* sh = shared;
+        shared = nullptr;  // recorded here, with its status checked
+        return shared_scratch_release(sh, stream);
+    }
     return OFH_SUCCESS;
 }
 
