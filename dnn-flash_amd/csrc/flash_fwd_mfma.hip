@@ -1133,18 +1133,33 @@ __device__ int build_tile_list_lds(const FwdArgs& a, int q0, int block_n, lds_in
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     int count = 0;
+    // The mask-block rows of each slice are the same for every thread (the
+    // query tile is the workgroup's); only the key tile differs. They are
+    // formed once, and by shifts where the block sizes are powers of two
+    // (the common case; a division costs some twenty VALU instructions).
+    const bool pow2 = (a.mask_qbs & (a.mask_qbs - 1)) == 0 && (a.mask_kbs & (a.mask_kbs - 1)) == 0;  // uniform
+    const int lq = __builtin_ctz((unsigned)a.mask_qbs), lk = __builtin_ctz((unsigned)a.mask_kbs);
+    int sq0[NWAVES], sq1[NWAVES], se[NWAVES];
+#pragma unroll
+    for (int w = 0; w < NWAVES; ++w) {
+        const int s0 = q0 + kQueriesPerWave * w, s1 = min(a.M, s0 + kQueriesPerWave);
+        se[w] = s1;
+        sq0[w] = s0 < s1 ? (pow2 ? s0 >> lq : s0 / a.mask_qbs) : 1;
+        sq1[w] = s0 < s1 ? (pow2 ? (s1 - 1) >> lq : (s1 - 1) / a.mask_qbs) : 0;  // empty slice: no rows
+    }
     for (int base = 0; base < a.num_k_tiles; base += NT) {
         const int kt = base + tid;
         unsigned any_bits = 0, full_bits = 0;
         if (kt < a.num_k_tiles) {
             const int k0 = kt * block_n, k1 = min(a.N, k0 + block_n);
+            const int kb0 = pow2 ? k0 >> lk : k0 / a.mask_kbs;
+            const int kb1 = pow2 ? (k1 - 1) >> lk : (k1 - 1) / a.mask_kbs;
 #pragma unroll
             for (int w = 0; w < NWAVES; ++w) {
-                const int s0 = q0 + kQueriesPerWave * w, s1 = min(a.M, s0 + kQueriesPerWave);
-                if (s0 >= s1) continue;
+                if (sq0[w] > sq1[w]) continue;
                 bool any, all;
-                classify_mask_slice(a.mask, a.mask_qbs, a.mask_kbs, a.mask_qb, a.mask_kb, a.causal, s0, s1,
-                                    k0, k1, any, all);
+                classify_mask_blocks(a.mask, a.mask_qbs, a.mask_kbs, a.mask_qb, a.mask_kb, a.causal, se[w], k0,
+                                     sq0[w], sq1[w], kb0, kb1, any, all);
                 any_bits |= (any ? 1u : 0u) << w;
                 full_bits |= (all ? 1u : 0u) << w;
             }

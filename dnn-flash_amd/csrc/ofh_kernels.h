@@ -126,6 +126,25 @@ __device__ inline void classify_mask_slice(const uint8_t* mask, int qbs, int kbs
     }
 }
 
+// classify_mask_slice with the slice's and the key tile's mask-block ranges
+// already formed: query blocks [qb0, qb1] of a slice ending at row q1
+// (exclusive), key blocks [kb0, kb1] of a tile starting at key k0.
+__device__ inline void classify_mask_blocks(const uint8_t* mask, int qbs, int kbs, int nqb, int nkb, int causal,
+                                            int q1, int k0, int qb0, int qb1, int kb0, int kb1, bool& any,
+                                            bool& all) {
+    any = false;
+    all = true;
+    for (int qb = qb0; qb <= qb1; ++qb) {
+        const int qe = min(q1, (qb + 1) * qbs);
+        for (int kb = kb0; kb <= kb1; ++kb) {
+            const int ks = max(k0, kb * kbs);
+            const bool allowed = qb < nqb && kb < nkb && mask[(int64_t)qb * nkb + kb] != 0;
+            any = any || (allowed && (!causal || ks <= qe - 1));
+            all = all && allowed;
+        }
+    }
+}
+
 struct TileListArgs {
     int M, N, block_m, block_n, causal;
     const uint8_t* mask;
