@@ -884,6 +884,11 @@ int ofh_attention_launch_info(const ofh_attention_params* p, ofh_launch_info* in
             pair_name = "flash_fwd_pair_split_kernel" + std::string(name).substr(lockstep.size());
             name = pair_name.c_str();
         }
+        // 16-bit block-mask calls with their lists built in LDS: a kernel of their own
+        if (r.lds_list && p->dtype != OFH_DTYPE_F32 && std::string(name).compare(0, lockstep.size(), lockstep) == 0) {
+            pair_name = "flash_fwd_lds_list_kernel" + std::string(name).substr(lockstep.size());
+            name = pair_name.c_str();
+        }
     } else {
         info->block_m = 1;
         info->block_n = 64;

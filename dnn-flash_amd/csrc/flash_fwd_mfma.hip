@@ -1401,6 +1401,19 @@ __global__ __launch_bounds__(NWAVES * 64, lockstep_min_blocks(D, NWAVES, MOD, LI
     }
 }
 
+// Block-mask calls whose lists are built in LDS (no key split, no global
+// list): the LDS-list path of the lockstep kernel as a kernel of its own, so
+// that its loop does not share registers with the global-list path.
+template <typename T, int D, int MOD>
+__global__ __launch_bounds__(256, lockstep_min_blocks(D, 4, MOD, true)) void flash_fwd_lds_list_kernel(FwdArgs a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char dyn_smem[];
+    using W = Wave32<T, D, MOD, true, 256, kBlockN16, 1>;
+    int bh, qt;
+    map_work((int)blockIdx.x, a.B * a.H, a.num_q_tiles, a.causal, bh, qt);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    lds_list_qtile<W, 4, MOD>(a, dyn_smem, bh, qt, qt * 4 * kQueriesPerWave, wave);
+}
+
 // Causal query tile pairs with a key split (FwdArgs::pair_split): workgroup s
 // of the pair (nqt-1-p, p) runs split s of both tiles, each tile cut into
 // num_splits ranges of its own length, so every workgroup runs about
@@ -1991,6 +2004,9 @@ static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
     const bool paired = pairs_causal_tiles(a.causal != 0, list) && a.num_splits == 1;
     if (list) {
         const size_t lds = list_kernel_lds_bytes(D, a.tile_counts == nullptr, a.num_k_tiles);
+        if (a.tile_counts == nullptr && a.num_splits == 1)
+            return general_mod ? launch(flash_fwd_lds_list_kernel<T, D, MOD_GENERAL>, 256, a, s, false, lds)
+                               : launch(flash_fwd_lds_list_kernel<T, D, MOD_PLAIN>, 256, a, s, false, lds);
         return general_mod ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, true, 4, false>, 256, a, s, false, lds)
                            : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, true, 4, false>, 256, a, s, false, lds);
     }

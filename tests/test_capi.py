@@ -183,6 +183,10 @@ def test_kernel_choice(ofh):
         (dict(dtype=F.DTYPE_F16, head_dim=64, mask_allowed=16, mask_query_block_size=64,
               mask_key_block_size=64, mask_query_blocks=4, mask_key_blocks=4),
          "flash_fwd_lockstep_kernel<f16,64,plain,list,4w>"),
+        # enough query tiles for no key split: the list is built in LDS, by a kernel of its own
+        (dict(dtype=F.DTYPE_F16, head_dim=64, shape=(1, 16, 16384, 16384), mask_allowed=16,
+              mask_query_block_size=64, mask_key_block_size=64, mask_query_blocks=256, mask_key_blocks=256),
+         "flash_fwd_lds_list_kernel<f16,64,plain,list,4w>"),
         (dict(dtype=F.DTYPE_BF16, head_dim=32), "flash_fwd_lockstep_kernel<bf16,32,plain,8w,128keys>"),
         (dict(dtype=F.DTYPE_F16, head_dim=32, softcap=5.0), "flash_fwd_lockstep_kernel<f16,32,mod,8w,2x64keys>"),
         (dict(dtype=F.DTYPE_BF16, head_dim=256), "flash_fwd_lockstep_kernel<bf16,256,plain,4w>"),
