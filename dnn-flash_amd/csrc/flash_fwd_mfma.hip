@@ -1377,7 +1377,11 @@ constexpr int lockstep_min_blocks(int D, int nwaves, int mod, bool list) {
     return nwaves == 8 ? 1 : D >= 160 ? 1 : (list && mod == MOD_PLAIN && D <= 64) ? 3 : 2;
 }
 
-template <typename T, int D, int MOD, bool LIST, int NWAVES, bool PAIRED, int BN = kBlockN16, int SB = 1>
+// SPLIT (query tiles not paired): the kernel may run a key split; calls with
+// one split take the instantiation without it, whose loop then keeps the
+// split's values out of its scalar registers (fewer spilled to vector lanes).
+template <typename T, int D, int MOD, bool LIST, int NWAVES, bool PAIRED, int BN = kBlockN16, int SB = 1,
+          bool SPLIT = true>
 __global__ __launch_bounds__(NWAVES * 64, lockstep_min_blocks(D, NWAVES, MOD, LIST)) void flash_fwd_lockstep_kernel(FwdArgs a) {
     using L = TileLayout<D, BN * SB>;
     // block-mask kernels: LDS sized at launch (list_kernel_lds_bytes)
@@ -1389,7 +1393,7 @@ __global__ __launch_bounds__(NWAVES * 64, lockstep_min_blocks(D, NWAVES, MOD, LI
         const int tiles = a.B * a.H * a.num_q_tiles;
         const int split = (int)blockIdx.x / tiles;
         map_work((int)blockIdx.x - split * tiles, a.B * a.H, a.num_q_tiles, a.causal, bh, qts[0]);
-        lockstep_qtile<T, D, MOD, LIST, NWAVES, BN, SB, true>(a, smem, bh, qts[0], split);
+        lockstep_qtile<T, D, MOD, LIST, NWAVES, BN, SB, SPLIT>(a, smem, bh, qts[0], split);
         return;
     }
     // (paired query tiles are never split)
@@ -2017,22 +2021,26 @@ static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
                                : launch(flash_fwd_pair_split_kernel<T, D, MOD_PLAIN, 4>, 256, a, s, true);
         if (general_mod)
             return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 4, true>, 256, a, s, true)
-                          : launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 4, false>, 256, a, s);
+                 : a.num_splits > 1 ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 4, false>, 256, a, s)
+                          : launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 4, false, kBlockN16, 1, false>, 256, a, s);
         return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 4, true>, 256, a, s, true)
-                      : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 4, false>, 256, a, s);
+             : a.num_splits > 1 ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 4, false>, 256, a, s)
+                      : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 4, false, kBlockN16, 1, false>, 256, a, s);
     } else {
         // score_mod: 64-key compute steps (two per staged tile at D = 32, 96, 160)
         constexpr int GSB = (D == 32 || (D & (D - 1)) != 0) ? 2 : 1;
         if (general_mod)
             return pair_split ? launch(flash_fwd_pair_split_kernel<T, D, MOD_GENERAL, 8, kBlockN16, GSB>, 512, a, s, true)
                  : paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8, true, kBlockN16, GSB>, 512, a, s, true)
-                          : launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8, false, kBlockN16, GSB>, 512, a, s);
+                 : a.num_splits > 1 ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8, false, kBlockN16, GSB>, 512, a, s)
+                          : launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 8, false, kBlockN16, GSB, false>, 512, a, s);
         // D <= 64: 128-key tiles; D = 128: 128 keys staged per barrier, two 64-key compute steps
         constexpr int BN = D <= 64 ? kBlockN16Wide : kBlockN16;
         constexpr int SB = D <= 64 ? 1 : kBlockN16Wide / kBlockN16;
         if (pair_split) return launch(flash_fwd_pair_split_kernel<T, D, MOD_PLAIN, 8, BN, SB>, 512, a, s, true);
         return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, true, BN, SB>, 512, a, s, true)
-                      : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, false, BN, SB>, 512, a, s);
+             : a.num_splits > 1 ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, false, BN, SB>, 512, a, s)
+                      : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, false, BN, SB, false>, 512, a, s);
     }
 }
 
