@@ -163,7 +163,7 @@ void choose_key_splits(const ofh_attention_params* p, Resolved& r) {
     r.key_splits = 1;
     r.split_tiles = 1 << 30;
     r.pair_split = false;
-    if (p->dtype == OFH_DTYPE_F32 && r.paired) return;
+    if (p->dtype == OFH_DTYPE_F32 && (r.paired || r.block_m == ofh::kRowsF32Narrow)) return;
     if (p->max_key_splits == 1) return;
     const bool rows32 = p->dtype == OFH_DTYPE_F32 && r.block_m == ofh::kRowsF32;
     const int64_t slots = kComputeUnits * workgroups_per_cu(p, r);
@@ -246,7 +246,8 @@ void no_key_split(const ofh_attention_params* p, Resolved& r) {
     r.key_splits = 1;
     r.split_tiles = 1 << 30;
     r.pair_split = false;
-    if (p->dtype == OFH_DTYPE_F32 && r.block_m == ofh::kRowsF32) return;  // 32-row blocks: no pairing, no list
+    // 32- and 16-row blocks: no pairing, no list
+    if (p->dtype == OFH_DTYPE_F32 && (r.block_m == ofh::kRowsF32 || r.block_m == ofh::kRowsF32Narrow)) return;
     const ofh::MfmaTiles t = ofh::flash_mfma_tiles(p->dtype, r.kdim, r.general_mod, r.tile_list, p->causal != 0);
     r.paired = t.paired;
     r.block_n = t.block_n;
@@ -323,6 +324,15 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
         r.paired = false;
         r.num_q_tiles = (int)((p->query_tokens + r.block_m - 1) / r.block_m);
         r.num_k_tiles = (int)((p->key_tokens + r.block_n - 1) / r.block_n);
+        // ... and with few keys as well, 16-row blocks of sixteen wavefronts
+        // that fold every key in the CU (no partial rows, no merge)
+        const int64_t blocks16 = (int64_t)p->batch * p->heads *
+                                 ((p->query_tokens + ofh::kRowsF32Narrow - 1) / ofh::kRowsF32Narrow);
+        if (r.kdim <= 64 && r.num_k_tiles <= ofh::kRows16MaxKeyTiles && blocks16 <= kComputeUnits) {
+            r.block_m = ofh::kRowsF32Narrow;
+            r.threads = 1024;
+            r.num_q_tiles = (int)((p->query_tokens + r.block_m - 1) / r.block_m);
+        }
     }
     const int64_t grid = (int64_t)p->batch * p->heads * r.num_q_tiles;
     if (grid > std::numeric_limits<int32_t>::max())
@@ -844,15 +854,17 @@ int ofh_attention_fwd_host(const ofh_attention_params* p, const float* q, const 
 }
 
 namespace {
-const char* rows32_kernel_name(int D, bool general) {
+const char* rows32_kernel_name(int D, bool general, bool narrow) {
     static const std::vector<std::string> names = [] {
         std::vector<std::string> v;
-        for (int d = 32; d <= 128; d += 32)
-            for (int gm = 0; gm < 2; ++gm)
-                v.push_back("flash_fwd_f32_rows32_kernel<" + std::to_string(d) + (gm ? ",general>" : ",plain>"));
+        for (int nr = 0; nr < 2; ++nr)
+            for (int d = 32; d <= 128; d += 32)
+                for (int gm = 0; gm < 2; ++gm)
+                    v.push_back(std::string(nr ? "flash_fwd_f32_rows16_kernel<" : "flash_fwd_f32_rows32_kernel<") +
+                                std::to_string(d) + (gm ? ",general>" : ",plain>"));
         return v;
     }();
-    return names[(size_t)(D / 32 - 1) * 2 + (general ? 1 : 0)].c_str();
+    return names[(size_t)(narrow ? 8 : 0) + (size_t)(D / 32 - 1) * 2 + (general ? 1 : 0)].c_str();
 }
 }  // namespace
 
@@ -874,8 +886,8 @@ int ofh_attention_launch_info(const ofh_attention_params* p, ofh_launch_info* in
                            r.key_splits;
         info->key_splits = r.key_splits;
         info->merge_in_launch = merge_in_launch(p, r) ? 1 : 0;
-        name = (p->dtype == OFH_DTYPE_F32 && r.block_m == ofh::kRowsF32)
-                   ? rows32_kernel_name(r.kdim, r.general_mod)
+        name = (p->dtype == OFH_DTYPE_F32 && (r.block_m == ofh::kRowsF32 || r.block_m == ofh::kRowsF32Narrow))
+                   ? rows32_kernel_name(r.kdim, r.general_mod, r.block_m == ofh::kRowsF32Narrow)
                    : ofh::flash_mfma_kernel_name(p->dtype, r.kdim, r.general_mod, r.tile_list);
         // 16-bit causal pairs with a key split run the same tiling in a kernel of their own
         static thread_local std::string pair_name;

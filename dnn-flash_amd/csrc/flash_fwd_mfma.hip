@@ -1893,6 +1893,221 @@ __global__ __launch_bounds__(kThreads32) void flash_fwd_f32_rows32_kernel(FwdArg
     }
 }
 
+// One 32-key tile of online softmax on two 16x16 score blocks (keys k0 + 16 kb
+// + 4 kq + i of query my_q in register i of block kb), in place; the four
+// lanes of a query (kq = 0..3) exchange their maxima. Returns alpha.
+template <bool GENERAL>
+__device__ __forceinline__ float online_softmax_16(const FwdArgs& a, f32x4 (&s)[2], bool need_mask, int my_q,
+                                                   int k0, int kq, float slope, const float* bias_row,
+                                                   float& m_run, float& l_run) {
+    float mx = kNegInf;
+    const bool row_out = GENERAL && my_q >= a.M;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int kj = k0 + 16 * kb + 4 * kq + i;
+            float x;
+            if (!GENERAL && !need_mask) {
+                x = s[kb][i] * a.scale_log2;
+            } else {
+                x = kNegInf;
+                if (!(row_out || (need_mask && elem_masked(a, my_q, kj))))
+                    x = GENERAL ? general_score(a, s[kb][i], my_q, kj, slope, bias_row) : s[kb][i] * a.scale_log2;
+            }
+            s[kb][i] = x;
+            mx = fmaxf(mx, x);
+        }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = (m_new == kNegInf) ? 0.0f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    m_run = m_new;
+    float lsum = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float p = __builtin_amdgcn_exp2f(s[kb][i] - m_use);
+            s[kb][i] = p;
+            lsum += p;
+        }
+    }
+    l_run = l_run * alpha + lsum;
+    return alpha;
+}
+
+// fp32 calls with few query rows and few keys: 16-row query blocks, one
+// workgroup of sixteen wavefronts per block (one workgroup per CU), no key
+// split, so no partial rows leave the CU. Wavefront w takes the block's
+// 32-key tiles w, w + 16, ... with K and V read straight into the operand
+// registers of v_mfma_f32_16x16x4f32 (the block's Q rows are read once per
+// workgroup, through LDS); the sixteen (m, l, O) states are folded through
+// LDS with the log-sum-exp rule (attention.cpp:661-674).
+//
+// Operand layout (lane l: n = l % 16, kq = l / 16). The head dim is permuted
+// inside each contraction, which leaves every sum unchanged:
+//   S^T = K Q^T: instruction c = 4 cc + t (< D/4) contracts over d = 16 cc +
+//     4 kq + t, so lane l holds K[key][16 cc + 4 kq, +4) and Q[q0 + n][16 cc
+//     + 4 kq, +4) as one 16-byte chunk per cc (the four lanes of a row read
+//     64 contiguous bytes); score block kb lands as
+//     S^T[k0 + 16 kb + 4 kq + i][q0 + n] in register i.
+//   O^T += V^T P^T: instruction (kb, i) contracts over keys k0 + 16 kb +
+//     4 kq + i, whose probability is the lane's own register i of block kb;
+//     output block db holds d = (D/16) m + db in row m, so lane l reads
+//     V[key][(D/16) n, +D/16) in one load, and holds O[q0 + n][(D/4) kq, +D/4)
+//     with d = (D/4) kq + e in element e = (D/16) i + db.
+constexpr int kWavesRows16 = 16;
+constexpr int kThreadsRows16 = kWavesRows16 * 64;
+
+template <int D, bool GENERAL>
+__global__ __launch_bounds__(kThreadsRows16) void flash_fwd_f32_rows16_kernel(FwdArgs a) {
+    static_assert(D == 32 || D == 64, "16-row fp32 blocks: D = 32 or 64");
+    constexpr int NC = D / 4;   // contraction floats per lane of S^T, O floats per lane
+    constexpr int NDB = D / 16;  // 16-row blocks of O^T
+    typedef float vrow_t __attribute__((ext_vector_type(NDB)));
+    constexpr int QSTR = D + 4;  // LDS row stride of the Q block (16 rows at distinct banks)
+    __shared__ __attribute__((aligned(16))) float fold_o[kWavesRows16 * 64 * NC];
+    __shared__ float fold_ml[kWavesRows16 * 32];
+    __shared__ __attribute__((aligned(16))) float q_lds[kRowsF32Narrow * QSTR];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 15, kq = lane >> 4;
+    int bh, qt;
+    map_work((int)blockIdx.x, a.B * a.H, a.num_q_tiles, a.causal, bh, qt);
+    const int b = bh / a.H, h = bh - b * a.H;
+    const float* __restrict__ Qp = (const float*)a.q + b * a.q_sb + h * a.q_sh;
+    const float* __restrict__ Kp = (const float*)a.k + b * a.k_sb + h * a.k_sh;
+    const float* __restrict__ Vp = (const float*)a.v + b * a.v_sb + h * a.v_sh;
+    const int q0 = qt * kRowsF32Narrow;
+    const int my_q = q0 + n;
+    const int kend = a.causal ? min(a.N, q0 + kRowsF32Narrow) : a.N;
+    const int ntiles = (kend + kBlockNF32 - 1) / kBlockNF32;
+
+    // K and V operands of tile it: rows past N read row N-1 (their scores
+    // are masked, so their probabilities are exactly 0); K chunks past D
+    // re-read the row's last chunk (Q is zero there), V columns past Dv its
+    // last columns (those output rows are not stored). V is requested once
+    // the K operands are consumed: requested together, both arrive later
+    // (measured), and one operand set at a time leaves registers to spare.
+    f32x4 kf[2][NC / 4];
+    vrow_t vf[2][4];
+    auto load_k = [&](int it) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const float* krow = Kp + (int64_t)min(it * kBlockNF32 + 16 * kb + n, a.N - 1) * a.k_sn;
+#pragma unroll
+            for (int cc = 0; cc < NC / 4; ++cc)
+                kf[kb][cc] = *(const f32x4*)(krow + min(16 * cc + 4 * kq, a.D - 4));
+        }
+    };
+    auto load_v = [&](int it) {
+        const int vc = min(NDB * n, a.Dv - NDB);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                vf[kb][i] = *(const vrow_t*)(Vp + (int64_t)min(it * kBlockNF32 + 16 * kb + 4 * kq + i, a.N - 1) *
+                                                       a.v_sn + vc);
+    };
+    // The Q block is read by the first 4 D threads (one 16-byte chunk each;
+    // rows past M and chunks past D are zero), after which the wavefront's
+    // first K tile is requested, and staged through LDS.
+    f32x4 qv = {0.f, 0.f, 0.f, 0.f};
+    const int qr = tid / (D / 4), qc = 4 * (tid - qr * (D / 4));
+    if (tid < 4 * D) {
+        qv = *(const f32x4*)(Qp + (int64_t)min(q0 + qr, a.M - 1) * a.q_sm + min(qc, a.D - 4));
+        if (q0 + qr >= a.M || qc >= a.D) qv = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (wave < ntiles) load_k(wave);
+    if (tid < 4 * D) *(f32x4*)(q_lds + qr * QSTR + qc) = qv;
+    __syncthreads();
+    float qf[NC];  // Q[my_q][16 cc + 4 kq + t] at 4 cc + t
+#pragma unroll
+    for (int cc = 0; cc < NC / 4; ++cc) {
+        const f32x4 u = *(const f32x4*)(q_lds + n * QSTR + 16 * cc + 4 * kq);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) qf[4 * cc + t] = u[t];
+    }
+    f32x4 o[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = kNegInf, l_run = 0.0f;
+    const float slope = (GENERAL && a.bias_kind == BIAS_ALIBI) ? a.alibi[h] : 0.0f;
+    const float* bias_row = nullptr;
+    if (GENERAL && a.bias_kind == BIAS_DENSE && my_q < a.M)
+        bias_row = a.bias + b * a.bias_sb + h * a.bias_sh + (int64_t)my_q * a.bias_sm;
+
+    for (int it = wave; it < ntiles; it += kWavesRows16) {
+        const int k0 = it * kBlockNF32;
+        if (it != wave) load_k(it);
+        f32x4 s[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+                s[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[kb][c >> 2][c & 3], qf[c], s[kb], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_v(it);
+        const bool need_mask = (k0 + kBlockNF32 > a.N) || (a.causal && k0 + kBlockNF32 - 1 > q0);
+        const float alpha =
+            online_softmax_16<GENERAL>(a, s, need_mask, my_q, k0, kq, slope, bias_row, m_run, l_run);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+                    o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[kb][i][db], s[kb][i], o[db], 0, 0, 0);
+    }
+
+    // Every wavefront (one that saw no tile has m = -inf, l = 0, O = 0) leaves
+    // its O in d order and the (m, l) of its 16 queries in LDS.
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
+    {
+        float* f = fold_o + (wave * 64 + lane) * NC;
+#pragma unroll
+        for (int c = 0; c < NC / 4; ++c) {
+            f32x4 val;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) val[t] = o[(4 * c + t) % NDB][(4 * c + t) / NDB];
+            *(f32x4*)(f + 4 * c) = val;
+        }
+        if (kq == 0) {
+            fold_ml[wave * 32 + n] = m_run;
+            fold_ml[wave * 32 + 16 + n] = l_run;
+        }
+    }
+    __syncthreads();
+    // Thread t folds 4 output columns: lane slot L = t / (NC / 4), chunk t % (NC / 4).
+    if (tid < 64 * (NC / 4)) {
+        const int L = tid / (NC / 4), c = tid - L * (NC / 4);
+        const int qn = L & 15, kqL = L >> 4;
+        float mg = kNegInf;
+#pragma unroll
+        for (int w = 0; w < kWavesRows16; ++w) mg = fmaxf(mg, fold_ml[w * 32 + qn]);
+        const float mu = mg == kNegInf ? 0.0f : mg;
+        float l = 0.0f;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < kWavesRows16; ++w) {
+            const float ww = __builtin_amdgcn_exp2f(fold_ml[w * 32 + qn] - mu);  // 0 for m = -inf
+            l += ww * fold_ml[w * 32 + 16 + qn];
+            acc += ww * *(const f32x4*)(fold_o + (w * 64 + L) * NC + 4 * c);
+        }
+        const int q = q0 + qn, d = NC * kqL + 4 * c;
+        if (q < a.M && d < a.Dv) {
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+            *(f32x4*)((float*)a.o + b * a.o_sb + h * a.o_sh + (int64_t)q * a.o_sm + d) = acc * inv;
+        }
+    }
+}
+
 // Merge of key-split partial rows in a launch of its own (no arrival
 // counters). A workgroup merges `rows` consecutive rows of one head (a power
 // of two, so they lie in one query tile): thread t takes (row, 4-column chunk)
@@ -2062,6 +2277,16 @@ hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipS
             default: return hipErrorInvalidValue;
         }
     } else if (dtype == DT_F32) {
+        if (a.split_bm == kRowsF32Narrow) {  // few query rows and keys: 16-row blocks, no key split
+            if (a.tile_counts != nullptr || a.mask != nullptr || a.num_splits != 1) return hipErrorInvalidValue;
+            switch (kd) {
+                case 32: return general_mod ? launch(flash_fwd_f32_rows16_kernel<32, true>, kThreadsRows16, a, s)
+                                            : launch(flash_fwd_f32_rows16_kernel<32, false>, kThreadsRows16, a, s);
+                case 64: return general_mod ? launch(flash_fwd_f32_rows16_kernel<64, true>, kThreadsRows16, a, s)
+                                            : launch(flash_fwd_f32_rows16_kernel<64, false>, kThreadsRows16, a, s);
+                default: return hipErrorInvalidValue;
+            }
+        }
         if (a.split_bm == kRowsF32) {  // few query rows: 32-row blocks (no block mask)
             if (a.tile_counts != nullptr) return hipErrorInvalidValue;
             switch (kd) {

@@ -18,6 +18,12 @@ constexpr int kQueriesPerWave = 32;
 // blocks, four wavefronts per block sharing its keys (flash_fwd_f32_rows32_kernel).
 constexpr int kRowsF32 = 32;
 constexpr int kRows32Below = 128;
+// Of those, calls at D <= 64 whose 16-row blocks fit one round of the CUs
+// (one workgroup each) and whose keys are at most kRows16MaxKeyTiles tiles of
+// 32 run 16-row blocks of sixteen wavefronts without a key split
+// (flash_fwd_f32_rows16_kernel).
+constexpr int kRowsF32Narrow = 16;
+constexpr int kRows16MaxKeyTiles = 32;
 
 struct MfmaTiles {
     int block_m;  // query rows per query tile

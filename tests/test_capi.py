@@ -173,7 +173,10 @@ def test_kernel_choice(ofh):
     cases = [
         (dict(dtype=F.DTYPE_BF16, head_dim=128), "flash_fwd_lockstep_kernel<bf16,128,plain,8w,2x64keys>"),
         (dict(dtype=F.DTYPE_F16, head_dim=64), "flash_fwd_lockstep_kernel<f16,64,plain,8w,128keys>"),
-        (dict(dtype=F.DTYPE_F32, head_dim=64), "flash_fwd_f32_rows32_kernel<64,plain>"),
+        (dict(dtype=F.DTYPE_F32, head_dim=64), "flash_fwd_f32_rows16_kernel<64,plain>"),
+        (dict(dtype=F.DTYPE_F32, head_dim=64, shape=(2, 3, 300, 1100)), "flash_fwd_f32_rows32_kernel<64,plain>"),
+        (dict(dtype=F.DTYPE_F32, head_dim=64, shape=(4, 4, 300, 200), softcap=5.0),
+         "flash_fwd_f32_rows32_kernel<64,general>"),
         (dict(dtype=F.DTYPE_F32, head_dim=64, shape=(4, 32, 512, 512)), "flash_fwd_mfma32_kernel<64,plain>"),
         (dict(dtype=F.DTYPE_F32, head_dim=128, softcap=5.0), "flash_fwd_f32_rows32_kernel<128,general>"),
         (dict(dtype=F.DTYPE_F32, head_dim=64, mask_allowed=16, mask_query_block_size=64,
@@ -193,7 +196,7 @@ def test_kernel_choice(ofh):
         (dict(dtype=F.DTYPE_F16, head_dim=256, mask_allowed=16, mask_query_block_size=64,
               mask_key_block_size=64, mask_query_blocks=5, mask_key_blocks=4),
          "flash_fwd_lockstep_kernel<f16,256,plain,list,4w>"),
-        (dict(dtype=F.DTYPE_F32, head_dim=32), "flash_fwd_f32_rows32_kernel<32,plain>"),
+        (dict(dtype=F.DTYPE_F32, head_dim=32), "flash_fwd_f32_rows16_kernel<32,plain>"),
         (dict(dtype=F.DTYPE_F32, head_dim=256), "rowwise_fwd_kernel"),
         (dict(dtype=F.DTYPE_F32, head_dim=96), "flash_fwd_f32_rows32_kernel<96,plain>"),
         (dict(dtype=F.DTYPE_F32, head_dim=96, shape=(8, 16, 1024, 300)), "flash_fwd_mfma32_kernel<96,plain>"),
@@ -205,7 +208,7 @@ def test_kernel_choice(ofh):
         (dict(dtype=F.DTYPE_BF16, head_dim=64, value_dim=128), "flash_fwd_lockstep_kernel<bf16,128,plain,8w,2x64keys>"),
         (dict(dtype=F.DTYPE_F16, head_dim=16), "flash_fwd_lockstep_kernel<f16,32,plain,8w,128keys>"),
         (dict(dtype=F.DTYPE_BF16, head_dim=192, value_dim=128, softcap=5.0), "flash_fwd_lockstep_kernel<bf16,192,mod,4w>"),
-        (dict(dtype=F.DTYPE_F32, head_dim=64, value_dim=48), "flash_fwd_f32_rows32_kernel<64,plain>"),
+        (dict(dtype=F.DTYPE_F32, head_dim=64, value_dim=48), "flash_fwd_f32_rows16_kernel<64,plain>"),
         (dict(dtype=F.DTYPE_F32, head_dim=40, shape=(8, 16, 1024, 300)), "flash_fwd_mfma32_kernel<64,plain>"),
         # not a multiple of the 16-byte row chunk, or beyond the kernels' head dims: rowwise
         (dict(dtype=F.DTYPE_BF16, head_dim=20), "rowwise_fwd_kernel"),
@@ -248,14 +251,22 @@ def test_kernel_choice(ofh):
     # without score_mod or block mask: 128 keys per staged tile
     assert F.launch_info(F.make_params(1, 2, 300, 200, 64, dtype=F.DTYPE_BF16)).block_n == 128
     assert F.launch_info(F.make_params(1, 2, 300, 200, 64, dtype=F.DTYPE_BF16, softcap=5.0)).block_n == 64
-    # fp32 with few query tiles: 32-row query blocks whose four wavefronts share
-    # the block's keys; each block's 16 tiles of 32 keys run as 4 workgroups
-    # (a tile per wavefront), merged in the same launch
+    # fp32 with few query tiles and few keys: 16-row query blocks of sixteen
+    # wavefronts, each block's 16 tiles of 32 keys one per wavefront, no key
+    # split (128 workgroups, no workspace)
     p = F.make_params(1, 4, 512, 512, 64, dtype=F.DTYPE_F32)
     info = F.launch_info(p)
+    assert info.block_m == 16 and info.block_n == 32 and info.threads == 1024
+    assert info.key_splits == 1 and info.workgroups == 4 * 32 and info.merge_in_launch == 0
+    assert F.workspace_bytes(p) == 0
+    # with more keys: 32-row query blocks whose four wavefronts share the
+    # block's keys; each block's 64 tiles of 32 keys run as 8 workgroups of 8
+    # tiles (512 workgroups: one round of two per CU), merged in the same launch
+    p = F.make_params(1, 4, 512, 2048, 64, dtype=F.DTYPE_F32)
+    info = F.launch_info(p)
     assert info.block_m == 32 and info.block_n == 32 and info.threads == 256
-    assert info.key_splits == 4 and info.workgroups == 4 * 16 * 4 and info.merge_in_launch == 1
-    assert F.workspace_bytes(p) >= 4 * 4 * 512 * 66 * 4
+    assert info.key_splits == 8 and info.workgroups == 4 * 16 * 8 and info.merge_in_launch == 1
+    assert F.workspace_bytes(p) >= 8 * 4 * 512 * 66 * 4
     # fp32 decode: one 32-row block per head, its 1024 tiles over 32 workgroups
     info = F.launch_info(F.make_params(1, 8, 1, 32768, 128, dtype=F.DTYPE_F32))
     assert info.block_m == 32 and info.key_splits == 32 and info.workgroups == 8 * 32

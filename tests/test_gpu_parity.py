@@ -96,10 +96,13 @@ def test_mfma_shapes(ofh, dt, D, causal, splits):
 def test_f32_row_blocks(ofh, D, causal):
     """fp32 calls with fewer than 128 query tiles of 128 rows run 32-row query
     blocks (four wavefronts share each block's keys and fold their states in
-    LDS); larger calls run the 128-row kernel. Both against the oracle, with
-    and without the key split (in-launch merge), plain and ALiBi + soft-cap."""
+    LDS), or, at D <= 64 with at most 32 key tiles of 32, 16-row blocks of
+    sixteen wavefronts without a key split; larger calls run the 128-row
+    kernel. All against the oracle, with and without the key split (in-launch
+    merge), plain and ALiBi + soft-cap."""
     F = ofh
-    for B, H, M, N, kind in [(1, 2, 200, 333, "rows32"), (8, 16, 200, 333, "mfma32")]:
+    small = "rows16" if D <= 64 else "rows32"
+    for B, H, M, N, kind in [(1, 2, 200, 333, small), (1, 2, 200, 1500, "rows32"), (8, 16, 200, 333, "mfma32")]:
         p = F.make_params(B, H, M, N, D, dtype=F.DTYPE_F32, causal=causal)
         name = F.launch_info(p).kernel_name.decode()
         assert kind in name, name
@@ -108,11 +111,38 @@ def test_f32_row_blocks(ofh, D, causal):
             out = run(ofh, dev, dt="f32", causal=causal, max_key_splits=splits)
             check(out, oracle_full(host, causal=causal), "f32",
                   f"{name} B{B} H{H} M{M} N{N} causal={causal} max_key_splits={splits}")
-        if kind == "rows32":
+        if kind != "mfma32":
             slopes = alibi_slopes(H)
             out = run(ofh, dev, dt="f32", causal=causal, slopes=slopes, softcap=5.0)
             check(out, oracle_full(host, causal=causal, slopes=slopes, softcap=5.0), "f32",
                   f"{name} ALiBi + soft-cap 5 causal={causal}")
+
+
+@pytest.mark.parametrize("D", [32, 64])
+def test_f32_rows16_edges(ofh, D):
+    """16-row fp32 blocks (sixteen wavefronts, one 32-key tile each per round,
+    no key split) at their edges: one row and one key, exact and ragged
+    block and tile counts, 32 key tiles (two per wavefront), causal rows with
+    fewer tiles than wavefronts, D != Dv, a dense bias; and the first shapes
+    past the planner's bounds, which take the 32-row kernel."""
+    F = ofh
+    for B, H, M, N, Dv in [(1, 1, 1, 1, D), (2, 3, 16, 32, D), (1, 2, 17, 33, D), (1, 3, 50, 1024, D),
+                           (2, 2, 31, 500, D - 16), (1, 1, 4096, 64, D)]:
+        name = F.launch_info(F.make_params(B, H, M, N, D, Dv, dtype=F.DTYPE_F32)).kernel_name.decode()
+        assert name == f"flash_fwd_f32_rows16_kernel<{D},plain>", (B, H, M, N, name)
+        dev, host = make_inputs("f32", B, H, M, N, D, Dv, seed=M + N)
+        for causal in (False, True):
+            out = run(ofh, dev, dt="f32", causal=causal)
+            check(out, oracle_full(host, causal=causal), "f32", f"rows16 B{B} H{H} M{M} N{N} D{D} Dv{Dv} causal={causal}")
+    B, H, M, N = 1, 2, 45, 300
+    dev, host = make_inputs("f32", B, H, M, N, D, seed=5)
+    bias = O.normal(11, (M, N), std=2.0)
+    out = run(ofh, dev, dt="f32", bias=bias, softcap=20.0, causal=True)
+    check(out, oracle_full(host, bias=bias, softcap=20.0, causal=True), "f32", f"rows16 D{D} dense bias + soft-cap")
+    # one key tile too many, or one 16-row block per CU too many: 32-row blocks
+    for B, H, M, N in [(1, 2, 40, 1025), (1, 1, 4097, 64)]:
+        name = F.launch_info(F.make_params(B, H, M, N, D, dtype=F.DTYPE_F32)).kernel_name.decode()
+        assert "rows32" in name, (B, H, M, N, name)
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
