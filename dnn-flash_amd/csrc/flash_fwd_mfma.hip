@@ -1969,7 +1969,11 @@ __global__ __launch_bounds__(kThreadsRows16) void flash_fwd_f32_rows16_kernel(Fw
     constexpr int NDB = D / 16;  // 16-row blocks of O^T
     typedef float vrow_t __attribute__((ext_vector_type(NDB)));
     constexpr int QSTR = D + 4;  // LDS row stride of the Q block (16 rows at distinct banks)
-    __shared__ __attribute__((aligned(16))) float fold_o[kWavesRows16 * 64 * NC];
+    constexpr int CPR = D / 4;   // 16-byte chunks per K row
+    constexpr int KT = kBlockNF32 * D;  // floats of one wavefront's K tile in LDS
+    static_assert(64 * NC <= KT, "a wavefront's folded state fits in its K tile");
+    // K tiles, one per wavefront (later its folded state); Q block; (m, l) per wavefront and query
+    __shared__ __attribute__((aligned(16))) float k_lds[kWavesRows16 * KT];
     __shared__ float fold_ml[kWavesRows16 * 32];
     __shared__ __attribute__((aligned(16))) float q_lds[kRowsF32Narrow * QSTR];
 
@@ -1986,23 +1990,25 @@ __global__ __launch_bounds__(kThreadsRows16) void flash_fwd_f32_rows16_kernel(Fw
     const int kend = a.causal ? min(a.N, q0 + kRowsF32Narrow) : a.N;
     const int ntiles = (kend + kBlockNF32 - 1) / kBlockNF32;
 
-    // K and V operands of tile it: rows past N read row N-1 (their scores
-    // are masked, so their probabilities are exactly 0); K chunks past D
-    // re-read the row's last chunk (Q is zero there), V columns past Dv its
-    // last columns (those output rows are not stored). V is requested once
-    // the K operands are consumed: requested together, both arrive later
-    // (measured), and one operand set at a time leaves registers to spare.
-    f32x4 kf[2][NC / 4];
-    vrow_t vf[2][4];
+    // K tile it is copied into the wavefront's LDS tile (global -> LDS, 1 KB
+    // of whole rows per instruction); chunk c of row r sits at slot
+    // c ^ kswz(r), so that the operand reads (16 rows at one chunk per 16
+    // lanes) meet distinct banks. V is read straight into the operand
+    // registers once the K operands are consumed. Rows past N read row N-1
+    // (their scores are masked, so their probabilities are exactly 0); K
+    // chunks past D re-read the row's last chunk (Q is zero there), V columns
+    // past Dv its last columns (those output rows are not stored).
+    float* const kw = k_lds + wave * KT;
+    auto kswz = [](int r) { return D == 64 ? (r & 15) : ((r >> 1) & 7); };
     auto load_k = [&](int it) {
+        const unsigned base = (unsigned)(uintptr_t)kw;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            const float* krow = Kp + (int64_t)min(it * kBlockNF32 + 16 * kb + n, a.N - 1) * a.k_sn;
-#pragma unroll
-            for (int cc = 0; cc < NC / 4; ++cc)
-                kf[kb][cc] = *(const f32x4*)(krow + min(16 * cc + 4 * kq, a.D - 4));
+        for (int j = 0; j < KT / 256; ++j) {
+            const int sl = 64 * j + lane, r = sl / CPR, c = (sl % CPR) ^ kswz(r);
+            dma16(Kp + (int64_t)min(it * kBlockNF32 + r, a.N - 1) * a.k_sn + min(4 * c, a.D - 4), base + 1024 * j);
         }
     };
+    vrow_t vf[2][4];
     auto load_v = [&](int it) {
         const int vc = min(NDB * n, a.Dv - NDB);
 #pragma unroll
@@ -2043,6 +2049,13 @@ __global__ __launch_bounds__(kThreadsRows16) void flash_fwd_f32_rows16_kernel(Fw
     for (int it = wave; it < ntiles; it += kWavesRows16) {
         const int k0 = it * kBlockNF32;
         if (it != wave) load_k(it);
+        wait_vm_loads();  // this wavefront's K copy has landed
+        f32x4 kf[2][NC / 4];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int cc = 0; cc < NC / 4; ++cc)
+                kf[kb][cc] = *(const f32x4*)(kw + (16 * kb + n) * D + 4 * ((4 * cc + kq) ^ kswz(16 * kb + n)));
         f32x4 s[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
         for (int c = 0; c < NC; ++c)
@@ -2066,11 +2079,12 @@ __global__ __launch_bounds__(kThreadsRows16) void flash_fwd_f32_rows16_kernel(Fw
     }
 
     // Every wavefront (one that saw no tile has m = -inf, l = 0, O = 0) leaves
-    // its O in d order and the (m, l) of its 16 queries in LDS.
+    // its O in d order (in its K tile, whose reads are done) and the (m, l)
+    // of its 16 queries in LDS.
     l_run += __shfl_xor(l_run, 16);
     l_run += __shfl_xor(l_run, 32);
     {
-        float* f = fold_o + (wave * 64 + lane) * NC;
+        float* f = kw + lane * NC;
 #pragma unroll
         for (int c = 0; c < NC / 4; ++c) {
             f32x4 val;
@@ -2098,7 +2112,7 @@ __global__ __launch_bounds__(kThreadsRows16) void flash_fwd_f32_rows16_kernel(Fw
         for (int w = 0; w < kWavesRows16; ++w) {
             const float ww = __builtin_amdgcn_exp2f(fold_ml[w * 32 + qn] - mu);  // 0 for m = -inf
             l += ww * fold_ml[w * 32 + 16 + qn];
-            acc += ww * *(const f32x4*)(fold_o + (w * 64 + L) * NC + 4 * c);
+            acc += ww * *(const f32x4*)(k_lds + w * KT + L * NC + 4 * c);
         }
         const int q = q0 + qn, d = NC * kqL + 4 * c;
         if (q < a.M && d < a.Dv) {
