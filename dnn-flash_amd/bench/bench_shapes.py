@@ -3,7 +3,9 @@
 
 Each --shape runs the attention forward on synthetic device-resident inputs
 (N(0,1), rounded to the dtype) on torch's current stream, W untimed calls then
-K timed calls between two HIP events on that stream, and prints one JSON line:
+K timed calls between two HIP events on that stream (ofh_attention_fwd called
+through ctypes with prepared arguments, so that the host side of a call stays
+shorter than the kernel), and prints one JSON line:
 microseconds per call (the whole call: every launch it makes), useful TFLOP/s
 (ofh_attention_useful_flops), the share of the bf16/fp16 (or fp32) dense MFMA
 peak, and the algorithmic HBM rate (Q, K, V read once, O written once) against
@@ -18,6 +20,7 @@ peak, and the algorithmic HBM rate (Q, K, V read once, O written once) against
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import sys
@@ -64,9 +67,15 @@ def main() -> int:
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
         scale = 1.0 / math.sqrt(D)
 
+        p.scale = scale
+        lib = F.lib()
+        argv = (ctypes.byref(p), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                ws.data_ptr() if ws_bytes else None, ws_bytes, torch.cuda.current_stream().cuda_stream)
+
         def call():
-            F.attention_fwd(q, k, v, scale=scale, causal=args.causal, out=out, workspace=ws,
-                            max_key_splits=args.max_key_splits, algorithm=algo)
+            rc = lib.ofh_attention_fwd(*argv)
+            if rc:
+                raise F.OfhError(rc, lib.ofh_last_error().decode())
 
         for _ in range(args.warmup):
             call()

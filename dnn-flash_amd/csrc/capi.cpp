@@ -325,10 +325,24 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
         r.num_q_tiles = (int)((p->query_tokens + r.block_m - 1) / r.block_m);
         r.num_k_tiles = (int)((p->key_tokens + r.block_n - 1) / r.block_n);
         // ... and with few keys as well, 16-row blocks of sixteen wavefronts
-        // that fold every key in the CU (no partial rows, no merge)
-        const int64_t blocks16 = (int64_t)p->batch * p->heads *
-                                 ((p->query_tokens + ofh::kRowsF32Narrow - 1) / ofh::kRowsF32Narrow);
-        if (r.kdim <= 64 && r.num_k_tiles <= ofh::kRows16MaxKeyTiles && blocks16 <= kComputeUnits) {
+        // that fold every key in the CU (no partial rows, no merge): up to 32
+        // key tiles of 32 (two per wavefront), or 64 where the blocks fill
+        // half the CUs. A wavefront's further tiles cost ~6 us each (loads not
+        // overlapped), against split workgroups that spread them over the
+        // CUs. Measured per call, 16-row blocks against 32-row blocks with the
+        // key split (D = 64): N512 8.8-9.4 against 10.0-15.3 us at 1 to 128
+        // blocks; N1024 15.0-15.4 against 14.9-16.2 at 4 to 32 blocks and
+        // 15.4-16.6 against 28.2-32.7 at 128 to 256; N2048 27.5 against 34.9
+        // at 128 blocks, 27.7 against 21.7 at 64 and 27.3 against 13.1 at 32;
+        // N4096 51.8 against 50.0 at 128. Causal blocks see the keys up to
+        // their last row only.
+        const int64_t nqb16 = ((int64_t)p->query_tokens + ofh::kRowsF32Narrow - 1) / ofh::kRowsF32Narrow;
+        const int64_t blocks16 = (int64_t)p->batch * p->heads * nqb16;
+        const int64_t keys16 = p->causal ? std::min<int64_t>((int64_t)p->key_tokens, nqb16 * ofh::kRowsF32Narrow)
+                                         : (int64_t)p->key_tokens;
+        const int64_t tiles16 = (keys16 + 31) / 32;
+        if (r.kdim <= 64 && blocks16 <= kComputeUnits &&
+            (tiles16 <= ofh::kRows16MaxKeyTiles || (tiles16 <= 2 * ofh::kRows16MaxKeyTiles && 2 * blocks16 >= kComputeUnits))) {
             r.block_m = ofh::kRowsF32Narrow;
             r.threads = 1024;
             r.num_q_tiles = (int)((p->query_tokens + r.block_m - 1) / r.block_m);

@@ -20,8 +20,8 @@ constexpr int kRowsF32 = 32;
 constexpr int kRows32Below = 128;
 // Of those, calls at D <= 64 whose 16-row blocks fit one round of the CUs
 // (one workgroup each) and whose keys are at most kRows16MaxKeyTiles tiles of
-// 32 run 16-row blocks of sixteen wavefronts without a key split
-// (flash_fwd_f32_rows16_kernel).
+// 32 (twice that where the blocks fill half the CUs) run 16-row blocks of
+// sixteen wavefronts without a key split (flash_fwd_f32_rows16_kernel).
 constexpr int kRowsF32Narrow = 16;
 constexpr int kRows16MaxKeyTiles = 32;
 

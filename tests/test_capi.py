@@ -259,10 +259,13 @@ def test_kernel_choice(ofh):
     assert info.block_m == 16 and info.block_n == 32 and info.threads == 1024
     assert info.key_splits == 1 and info.workgroups == 4 * 32 and info.merge_in_launch == 0
     assert F.workspace_bytes(p) == 0
+    # 64 key tiles with 128 16-row blocks (half the CUs) still take them
+    info = F.launch_info(F.make_params(1, 4, 512, 2048, 64, dtype=F.DTYPE_F32))
+    assert info.block_m == 16 and info.key_splits == 1
     # with more keys: 32-row query blocks whose four wavefronts share the
-    # block's keys; each block's 64 tiles of 32 keys run as 8 workgroups of 8
-    # tiles (512 workgroups: one round of two per CU), merged in the same launch
-    p = F.make_params(1, 4, 512, 2048, 64, dtype=F.DTYPE_F32)
+    # block's keys; each block's 128 tiles of 32 keys run as 8 workgroups of
+    # 16 tiles (512 workgroups: one round of two per CU), merged in the same launch
+    p = F.make_params(1, 4, 512, 4096, 64, dtype=F.DTYPE_F32)
     info = F.launch_info(p)
     assert info.block_m == 32 and info.block_n == 32 and info.threads == 256
     assert info.key_splits == 8 and info.workgroups == 4 * 16 * 8 and info.merge_in_launch == 1

@@ -102,7 +102,7 @@ def test_f32_row_blocks(ofh, D, causal):
     merge), plain and ALiBi + soft-cap."""
     F = ofh
     small = "rows16" if D <= 64 else "rows32"
-    for B, H, M, N, kind in [(1, 2, 200, 333, small), (1, 2, 200, 1500, "rows32"), (8, 16, 200, 333, "mfma32")]:
+    for B, H, M, N, kind in [(1, 2, 200, 333, small), (1, 1, 1100, 1500, "rows32"), (8, 16, 200, 333, "mfma32")]:
         p = F.make_params(B, H, M, N, D, dtype=F.DTYPE_F32, causal=causal)
         name = F.launch_info(p).kernel_name.decode()
         assert kind in name, name
@@ -127,11 +127,12 @@ def test_f32_rows16_edges(ofh, D):
     past the planner's bounds, which take the 32-row kernel."""
     F = ofh
     for B, H, M, N, Dv in [(1, 1, 1, 1, D), (2, 3, 16, 32, D), (1, 2, 17, 33, D), (1, 3, 50, 1024, D),
-                           (2, 2, 31, 500, D - 16), (1, 1, 4096, 64, D)]:
-        name = F.launch_info(F.make_params(B, H, M, N, D, Dv, dtype=F.DTYPE_F32)).kernel_name.decode()
-        assert name == f"flash_fwd_f32_rows16_kernel<{D},plain>", (B, H, M, N, name)
+                           (2, 2, 31, 500, D - 16), (1, 1, 4096, 64, D), (1, 8, 250, 2048, D)]:
         dev, host = make_inputs("f32", B, H, M, N, D, Dv, seed=M + N)
         for causal in (False, True):
+            name = F.launch_info(F.make_params(B, H, M, N, D, Dv, dtype=F.DTYPE_F32,
+                                               causal=causal)).kernel_name.decode()
+            assert name == f"flash_fwd_f32_rows16_kernel<{D},plain>", (B, H, M, N, causal, name)
             out = run(ofh, dev, dt="f32", causal=causal)
             check(out, oracle_full(host, causal=causal), "f32", f"rows16 B{B} H{H} M{M} N{N} D{D} Dv{Dv} causal={causal}")
     B, H, M, N = 1, 2, 45, 300
@@ -139,8 +140,15 @@ def test_f32_rows16_edges(ofh, D):
     bias = O.normal(11, (M, N), std=2.0)
     out = run(ofh, dev, dt="f32", bias=bias, softcap=20.0, causal=True)
     check(out, oracle_full(host, bias=bias, softcap=20.0, causal=True), "f32", f"rows16 D{D} dense bias + soft-cap")
-    # one key tile too many, or one 16-row block per CU too many: 32-row blocks
-    for B, H, M, N in [(1, 2, 40, 1025), (1, 1, 4097, 64)]:
+    # causal rows see the keys up to their own: 2000 keys, 7 blocks of 16 rows, 4 key tiles
+    B, H, M, N = 1, 2, 100, 2000
+    assert "rows16" in F.launch_info(F.make_params(B, H, M, N, D, dtype=F.DTYPE_F32, causal=True)).kernel_name.decode()
+    dev, host = make_inputs("f32", B, H, M, N, D, seed=9)
+    out = run(ofh, dev, dt="f32", causal=True)
+    check(out, oracle_full(host, causal=True), "f32", f"rows16 D{D} causal M{M} N{N}")
+    # one key tile too many (33 of 32, or 65 of 64 with 128 blocks), or one
+    # 16-row block per CU too many: 32-row blocks
+    for B, H, M, N in [(1, 2, 40, 1025), (1, 8, 250, 2049), (1, 1, 4097, 64)]:
         name = F.launch_info(F.make_params(B, H, M, N, D, dtype=F.DTYPE_F32)).kernel_name.decode()
         assert "rows32" in name, (B, H, M, N, name)
 
