@@ -1140,12 +1140,14 @@ __device__ int build_tile_list_lds(const FwdArgs& a, int q0, int block_n, lds_in
     const bool pow2 = (a.mask_qbs & (a.mask_qbs - 1)) == 0 && (a.mask_kbs & (a.mask_kbs - 1)) == 0;  // uniform
     const int lq = __builtin_ctz((unsigned)a.mask_qbs), lk = __builtin_ctz((unsigned)a.mask_kbs);
     int sq0[NWAVES], sq1[NWAVES], se[NWAVES];
+    bool one_qb = true;  // every slice within one mask-block row (uniform)
 #pragma unroll
     for (int w = 0; w < NWAVES; ++w) {
         const int s0 = q0 + kQueriesPerWave * w, s1 = min(a.M, s0 + kQueriesPerWave);
         se[w] = s1;
         sq0[w] = s0 < s1 ? (pow2 ? s0 >> lq : s0 / a.mask_qbs) : 1;
         sq1[w] = s0 < s1 ? (pow2 ? (s1 - 1) >> lq : (s1 - 1) / a.mask_qbs) : 0;  // empty slice: no rows
+        one_qb = one_qb && sq0[w] >= sq1[w];
     }
     for (int base = 0; base < a.num_k_tiles; base += NT) {
         const int kt = base + tid;
@@ -1154,14 +1156,33 @@ __device__ int build_tile_list_lds(const FwdArgs& a, int q0, int block_n, lds_in
             const int k0 = kt * block_n, k1 = min(a.N, k0 + block_n);
             const int kb0 = pow2 ? k0 >> lk : k0 / a.mask_kbs;
             const int kb1 = pow2 ? (k1 - 1) >> lk : (k1 - 1) / a.mask_kbs;
+            if (one_qb && kb0 == kb1) {
+                // One mask byte per slice (the common case: blocks no smaller
+                // than a slice and a key tile), all requested before any is
+                // used: the loops below would wait for each in turn. Same
+                // rule as classify_mask_blocks.
+                unsigned char mb[NWAVES];
 #pragma unroll
-            for (int w = 0; w < NWAVES; ++w) {
-                if (sq0[w] > sq1[w]) continue;
-                bool any, all;
-                classify_mask_blocks(a.mask, a.mask_qbs, a.mask_kbs, a.mask_qb, a.mask_kb, a.causal, se[w], k0,
-                                     sq0[w], sq1[w], kb0, kb1, any, all);
-                any_bits |= (any ? 1u : 0u) << w;
-                full_bits |= (all ? 1u : 0u) << w;
+                for (int w = 0; w < NWAVES; ++w)
+                    mb[w] = a.mask[(int64_t)min(sq0[w], a.mask_qb - 1) * a.mask_kb + min(kb0, a.mask_kb - 1)];
+#pragma unroll
+                for (int w = 0; w < NWAVES; ++w) {
+                    const int qe = min(se[w], (sq0[w] + 1) * a.mask_qbs);
+                    const bool allowed = sq0[w] <= sq1[w] && sq0[w] < a.mask_qb && kb0 < a.mask_kb && mb[w] != 0;
+                    const bool any = allowed && (!a.causal || k0 <= qe - 1);
+                    any_bits |= (any ? 1u : 0u) << w;
+                    full_bits |= (allowed ? 1u : 0u) << w;
+                }
+            } else {
+#pragma unroll
+                for (int w = 0; w < NWAVES; ++w) {
+                    if (sq0[w] > sq1[w]) continue;
+                    bool any, all;
+                    classify_mask_blocks(a.mask, a.mask_qbs, a.mask_kbs, a.mask_qb, a.mask_kb, a.causal, se[w],
+                                         k0, sq0[w], sq1[w], kb0, kb1, any, all);
+                    any_bits |= (any ? 1u : 0u) << w;
+                    full_bits |= (all ? 1u : 0u) << w;
+                }
             }
         }
         const unsigned long long bal = __ballot(any_bits != 0);

@@ -195,6 +195,13 @@ def test_block_masks(ofh, dt):
             out = run(ofh, dev, dt=dt, causal=causal, mask=mask, mbs=mbs)
             ref = oracle_full(host, causal=causal, mask=mask, mbs=mbs)
             check(out, ref, dt, f"{dt} mask {mbs} causal={causal}")
+    # a bitmap with fewer blocks than the problem: blocks past its end are disallowed
+    mask = (rng.random((3, 4)) < 0.7).astype(np.uint8)
+    mask[:, 0] = 1
+    for causal in (False, True):
+        out = run(ofh, dev, dt=dt, causal=causal, mask=mask, mbs=(64, 64))
+        check(out, oracle_full(host, causal=causal, mask=mask, mbs=(64, 64)), dt,
+              f"{dt} mask (64, 64) of 3 x 4 blocks causal={causal}")
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
@@ -321,11 +328,12 @@ def test_explicit_workspace(ofh):
 
 
 KEY_SPLIT_CASES = {
-    # name: (B, H, M, N, D, causal, extras)
-    "plain": (1, 2, 300, 1000, 64, False, {}),
+    # name: (B, H, M, N, D, causal, extras); D = 64 calls with few keys take
+    # 16-row blocks without a split, so these have more keys or D > 64
+    "plain": (1, 2, 300, 2100, 64, False, {}),
     "causal": (1, 2, 1000, 1000, 128, True, {}),
-    "wide_causal": (1, 3, 700, 260, 64, True, {}),
-    "alibi_softcap": (1, 2, 500, 900, 64, True, {"alibi": True, "softcap": 20.0}),
+    "wide_causal": (1, 3, 700, 260, 96, True, {}),
+    "alibi_softcap": (1, 2, 500, 900, 96, True, {"alibi": True, "softcap": 20.0}),
     "block_mask": (1, 2, 600, 800, 64, True, {"mask": (64, 64)}),
     "masked_rows": (1, 1, 512, 768, 64, False, {"mask": (128, 64), "zero_qblock": 1}),
 }
@@ -339,16 +347,14 @@ def test_key_split_fp32(ofh, name):
     fully masked rows stay 0, and the workspace query covers the partial rows."""
     F = ofh
     B, H, M, N, D, causal, ex = KEY_SPLIT_CASES[name]
-    p = F.make_params(B, H, M, N, D, dtype=F.DTYPE_F32, causal=causal)
-    info = F.launch_info(p)
-    assert info.key_splits > 1, f"{name}: expected a key split, got {info.key_splits}"
-    assert F.workspace_bytes(p) >= info.key_splits * B * H * M * (D + 2) * 4
     dev, host = make_inputs("f32", B, H, M, N, D, seed=len(name))
-    kw, rk = {}, {}
+    kw, rk, pk = {}, {}, {}
     if ex.get("alibi"):
         kw["slopes"] = rk["slopes"] = alibi_slopes(H)
     if "softcap" in ex:
         kw["softcap"] = rk["softcap"] = ex["softcap"]
+        pk["softcap"] = ex["softcap"]
+    tmask = None
     if "mask" in ex:
         mbs = ex["mask"]
         qb, kb = -(-M // mbs[0]), -(-N // mbs[1])
@@ -358,7 +364,15 @@ def test_key_split_fp32(ofh, name):
             mask[ex["zero_qblock"], :] = 0
         kw.update(mask=mask, mbs=mbs)
         rk.update(mask=mask, mbs=mbs)
-    print(f"key split {name}: splits {info.key_splits} workgroups {info.workgroups}", flush=True)
+        tmask = torch.from_numpy(mask).cuda()
+        pk.update(mask_allowed=tmask.data_ptr(), mask_query_block_size=mbs[0], mask_key_block_size=mbs[1],
+                  mask_query_blocks=qb, mask_key_blocks=kb)
+    p = F.make_params(B, H, M, N, D, dtype=F.DTYPE_F32, causal=causal, **pk)
+    info = F.launch_info(p)
+    assert info.key_splits > 1, f"{name}: expected a key split, got {info.key_splits}"
+    assert F.workspace_bytes(p) >= info.key_splits * B * H * M * (D + 2) * 4
+    print(f"key split {name}: {info.kernel_name.decode()} splits {info.key_splits} workgroups {info.workgroups}",
+          flush=True)
     out = run(F, dev, dt="f32", causal=causal, **kw)
     check(out, oracle_full(host, causal=causal, **rk), "f32", f"key split {name}")
     if "zero_qblock" in ex:
@@ -368,7 +382,7 @@ def test_key_split_fp32(ofh, name):
 
 def test_key_split_workspace(ofh):
     F = ofh
-    B, H, M, N, D = 1, 2, 256, 1024, 64
+    B, H, M, N, D = 1, 2, 256, 2100, 64
     p = F.make_params(B, H, M, N, D, dtype=F.DTYPE_F32)
     assert F.launch_info(p).key_splits > 1
     need = F.workspace_bytes(p)
@@ -454,8 +468,8 @@ def test_host_entry_concurrent_threads(ofh):
     result meets the bar against the oracle of its own inputs."""
     import threading
     F = ofh
-    B, H, M, N, D = 1, 2, 256, 768, 64
-    p = F.make_params(B, H, M, N, D, dtype=F.DTYPE_F32)
+    B, H, M, N, D = 1, 2, 256, 768, 96
+    p = F.make_params(B, H, M, N, D, dtype=F.DTYPE_F32, causal=True, scale=0.125)
     assert F.launch_info(p).key_splits > 1
     jobs = []
     for t in range(4):

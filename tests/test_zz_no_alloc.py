@@ -53,7 +53,7 @@ def test_noalloc_matches_fwd(ofh):
         ("fp32 block mask, smaller", "f32", 1, 2, 1024, 1024, 64, True, True, 1),
         ("bf16 key split", "bf16", 1, 2, 64, 16384, 128, False, False, 0),
         ("bf16 key split, smaller", "bf16", 1, 1, 1, 4000, 128, False, False, 0),  # merged in the launch
-        ("fp32 key split", "f32", 1, 4, 256, 1024, 64, False, False, 0),
+        ("fp32 key split", "f32", 1, 4, 256, 2100, 64, False, False, 0),
         ("fp32 key split, smaller", "f32", 1, 2, 64, 512, 128, False, False, 0),
     ]
     stream = torch.cuda.Stream()
