@@ -910,6 +910,13 @@ int ofh_attention_launch_info(const ofh_attention_params* p, ofh_launch_info* in
             pair_name = "flash_fwd_pair_split_kernel" + std::string(name).substr(lockstep.size());
             name = pair_name.c_str();
         }
+        // 16-bit causal query tiles run in pairs per workgroup (nqt-1-p, p)
+        if (r.paired && !r.pair_split && p->dtype != OFH_DTYPE_F32 &&
+            std::string(name).compare(0, lockstep.size(), lockstep) == 0) {
+            pair_name = std::string(name);
+            pair_name.insert(pair_name.size() - 1, ",paired");
+            name = pair_name.c_str();
+        }
         // 16-bit block-mask calls with their lists built in LDS: a kernel of their own
         if (r.lds_list && p->dtype != OFH_DTYPE_F32 && std::string(name).compare(0, lockstep.size(), lockstep) == 0) {
             pair_name = "flash_fwd_lds_list_kernel" + std::string(name).substr(lockstep.size());
