@@ -1963,10 +1963,10 @@ __device__ __forceinline__ float online_softmax_16(const FwdArgs& a, f32x4 (&s)[
 // fp32 calls with few query rows and few keys: 16-row query blocks, one
 // workgroup of sixteen wavefronts per block (one workgroup per CU), no key
 // split, so no partial rows leave the CU. Wavefront w takes the block's
-// 32-key tiles w, w + 16, ... with K and V read straight into the operand
-// registers of v_mfma_f32_16x16x4f32 (the block's Q rows are read once per
-// workgroup, through LDS); the sixteen (m, l, O) states are folded through
-// LDS with the log-sum-exp rule (attention.cpp:661-674).
+// 32-key tiles w, w + 16, ... on v_mfma_f32_16x16x4f32: its K tile copied
+// into LDS, its V tile read straight into the operand registers, the block's
+// Q rows read once per workgroup through LDS; the sixteen (m, l, O) states
+// are folded through LDS with the log-sum-exp rule (attention.cpp:661-674).
 //
 // Operand layout (lane l: n = l % 16, kq = l / 16). The head dim is permuted
 // inside each contraction, which leaves every sum unchanged:
