@@ -259,6 +259,19 @@ def test_kernel_choice(ofh):
     assert info.block_m == 16 and info.block_n == 32 and info.threads == 1024
     assert info.key_splits == 1 and info.workgroups == 4 * 32 and info.merge_in_launch == 0
     assert F.workspace_bytes(p) == 0
+    # 16-row blocks at the planner's bounds: at most 32 key tiles of 32, or 64
+    # where the blocks fill half the CUs; one block per CU at most; causal
+    # blocks see the keys up to their last row; D <= 64 only
+    for (B, H, M, N, D, causal), rows in [((1, 2, 40, 1024, 64, 0), 16), ((1, 2, 40, 1025, 64, 0), 32),
+                                          ((1, 8, 250, 2048, 64, 0), 16), ((1, 8, 250, 2049, 64, 0), 32),
+                                          ((1, 1, 4096, 64, 64, 0), 16), ((1, 1, 4097, 64, 64, 0), 32),
+                                          ((1, 2, 100, 2000, 64, 1), 16), ((1, 2, 100, 2000, 64, 0), 32),
+                                          ((1, 2, 100, 300, 96, 0), 32), ((1, 2, 100, 300, 32, 1), 16)]:
+        info = F.launch_info(F.make_params(B, H, M, N, D, dtype=F.DTYPE_F32, causal=causal))
+        assert info.block_m == rows, (B, H, M, N, D, causal, info.block_m)
+        if rows == 16:
+            assert info.key_splits == 1 and info.threads == 1024
+            assert info.kernel_name.decode() == f"flash_fwd_f32_rows16_kernel<{D},plain>"
     # 64 key tiles with 128 16-row blocks (half the CUs) still take them
     info = F.launch_info(F.make_params(1, 4, 512, 2048, 64, dtype=F.DTYPE_F32))
     assert info.block_m == 16 and info.key_splits == 1
