@@ -1489,7 +1489,7 @@ struct Mfma32Tiles {
 
 // Query tile qt of head bh, key split `split` (the whole key range without
 // one), on the workgroup's LDS `lds` (2 * STAGE floats).
-template <int D, bool GENERAL, int NB>
+template <int D, bool GENERAL, int NB, bool LISTS = true>
 __device__ __forceinline__ void mfma32_qtile(const FwdArgs& a, float* lds, int bh, int qt, int split) {
     using TL = Mfma32Tiles<D, NB>;
     constexpr int BN = TL::BN;
@@ -1528,7 +1528,7 @@ __device__ __forceinline__ void mfma32_qtile(const FwdArgs& a, float* lds, int b
 
     int ntiles;
     const int* list = nullptr;
-    if (a.tile_counts != nullptr) {
+    if (LISTS && a.tile_counts != nullptr) {
         ntiles = a.tile_counts[qt];
         list = a.tile_entries + (int64_t)qt * a.num_k_tiles;
     } else {
@@ -1690,18 +1690,21 @@ __device__ __forceinline__ void mfma32_qtile(const FwdArgs& a, float* lds, int b
     }
 }
 
-template <int D, bool GENERAL, int NB = 1>
+// PAIRS_ONLY: causal calls without a block mask, which always run query tile
+// pairs: an instantiation without the unpaired and list paths, whose values
+// then stay out of its scalar registers (57 -> 10 spilled at D = 64; +1 %).
+template <int D, bool GENERAL, int NB = 1, bool PAIRS_ONLY = false>
 __global__ __launch_bounds__(kThreads32) void flash_fwd_mfma32_kernel(FwdArgs a) {
     __shared__ __attribute__((aligned(16))) float lds[2 * Mfma32Tiles<D, NB>::STAGE];
-    if (a.pair_split) {  // causal query tile pairs, split s of both tiles
+    if (PAIRS_ONLY || a.pair_split) {  // causal query tile pairs, split s of both tiles
         const int pairs = a.B * a.H * ((a.num_q_tiles + 1) / 2);
         const int split = (int)blockIdx.x / pairs;
         int bh, qa, qb;
         map_work_pair((int)blockIdx.x - split * pairs, a.B * a.H, a.num_q_tiles, bh, qa, qb);
-        mfma32_qtile<D, GENERAL, NB>(a, lds, bh, qa, split);
+        mfma32_qtile<D, GENERAL, NB, !PAIRS_ONLY>(a, lds, bh, qa, split);
         if (qb >= 0) {
             __syncthreads();  // LDS stages are reused
-            mfma32_qtile<D, GENERAL, NB>(a, lds, bh, qb, split);
+            mfma32_qtile<D, GENERAL, NB, !PAIRS_ONLY>(a, lds, bh, qb, split);
         }
         return;
     }
@@ -2294,6 +2297,17 @@ static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
     }
 }
 
+// fp32 128-row query tiles: causal pairs without a block mask take the
+// pairs-only instantiation.
+template <int D>
+static hipError_t launch32(const FwdArgs& a, bool general_mod, hipStream_t s) {
+    if (a.pair_split && a.tile_counts == nullptr)
+        return general_mod ? launch(flash_fwd_mfma32_kernel<D, true, kTilesF32, true>, kThreads32, a, s, true)
+                           : launch(flash_fwd_mfma32_kernel<D, false, kTilesF32, true>, kThreads32, a, s, true);
+    return general_mod ? launch(flash_fwd_mfma32_kernel<D, true, kTilesF32>, kThreads32, a, s, a.pair_split != 0)
+                       : launch(flash_fwd_mfma32_kernel<D, false, kTilesF32>, kThreads32, a, s, a.pair_split != 0);
+}
+
 hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipStream_t s) {
     // the kernel's head dim: D and Dv rounded up (the kernels zero-pad Q and
     // mask the stores past Dv)
@@ -2336,18 +2350,13 @@ hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipS
                 default: return hipErrorInvalidValue;
             }
         }
-        if (kd == 96)
-            return general_mod ? launch(flash_fwd_mfma32_kernel<96, true, kTilesF32>, kThreads32, a, s, a.pair_split != 0)
-                               : launch(flash_fwd_mfma32_kernel<96, false, kTilesF32>, kThreads32, a, s, a.pair_split != 0);
-        if (kd == 32)
-            return general_mod ? launch(flash_fwd_mfma32_kernel<32, true, kTilesF32>, kThreads32, a, s, a.pair_split != 0)
-                               : launch(flash_fwd_mfma32_kernel<32, false, kTilesF32>, kThreads32, a, s, a.pair_split != 0);
-        if (kd == 64)
-            return general_mod ? launch(flash_fwd_mfma32_kernel<64, true, kTilesF32>, kThreads32, a, s, a.pair_split != 0)
-                               : launch(flash_fwd_mfma32_kernel<64, false, kTilesF32>, kThreads32, a, s, a.pair_split != 0);
-        if (kd == 128)
-            return general_mod ? launch(flash_fwd_mfma32_kernel<128, true, kTilesF32>, kThreads32, a, s, a.pair_split != 0)
-                               : launch(flash_fwd_mfma32_kernel<128, false, kTilesF32>, kThreads32, a, s, a.pair_split != 0);
+        switch (kd) {
+            case 32: return launch32<32>(a, general_mod, s);
+            case 64: return launch32<64>(a, general_mod, s);
+            case 96: return launch32<96>(a, general_mod, s);
+            case 128: return launch32<128>(a, general_mod, s);
+            default: break;
+        }
     }
     return hipErrorInvalidValue;
 }
