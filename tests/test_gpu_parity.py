@@ -188,7 +188,9 @@ def test_block_masks(ofh, dt):
     rng = np.random.default_rng(3)
     M, N, D = 300, 350, 64
     dev, host = make_inputs(dt, 1, 2, M, N, D, seed=11)
-    for mbs in [(64, 64), (16, 32), (100, 7), (1, 1), (128, 64)]:
+    # (64, 64), (128, 64), (96, 192): every 32-row slice and 64-key tile within one mask block (one
+    # mask byte per slice when the lists are built; 96 and 192 by division); the others span blocks
+    for mbs in [(64, 64), (16, 32), (100, 7), (1, 1), (128, 64), (96, 192), (48, 64)]:
         qb, kb = -(-M // mbs[0]), -(-N // mbs[1])
         mask = (rng.random((qb, kb)) < 0.4).astype(np.uint8)
         for causal in (False, True):
