@@ -148,7 +148,7 @@ int workgroups_per_cu(const ofh_attention_params* p, const Resolved& r) {
     if (r.tile_list && !r.general_mod && r.kdim <= 64) return 3;
     return r.kdim < 160 ? 2 : 1;
 }
-constexpr int64_t kComputeUnits = 256;  // MI355X
+using ofh::kComputeUnits;
 
 // Key split for calls with fewer query tiles than the GPU runs at once: every
 // query tile's K/V tile steps are cut into ranges of `per` steps, one
@@ -248,7 +248,8 @@ void no_key_split(const ofh_attention_params* p, Resolved& r) {
     r.pair_split = false;
     // 32- and 16-row blocks: no pairing, no list
     if (p->dtype == OFH_DTYPE_F32 && (r.block_m == ofh::kRowsF32 || r.block_m == ofh::kRowsF32Narrow)) return;
-    const ofh::MfmaTiles t = ofh::flash_mfma_tiles(p->dtype, r.kdim, r.general_mod, r.tile_list, p->causal != 0);
+    const ofh::MfmaTiles t = ofh::flash_mfma_tiles(p->dtype, r.kdim, r.general_mod, r.tile_list, p->causal != 0,
+                                                   (int64_t)p->batch * p->heads, p->query_tokens);
     r.paired = t.paired;
     r.block_n = t.block_n;
     r.num_k_tiles = (int)((p->key_tokens + r.block_n - 1) / r.block_n);
@@ -307,7 +308,8 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
     }
     r.algorithm = OFH_ALGO_FLASH_MFMA;
     const ofh::MfmaTiles tiles =
-        ofh::flash_mfma_tiles(p->dtype, r.kdim, r.general_mod, p->mask_allowed != nullptr, p->causal != 0);
+        ofh::flash_mfma_tiles(p->dtype, r.kdim, r.general_mod, p->mask_allowed != nullptr, p->causal != 0,
+                              (int64_t)p->batch * p->heads, p->query_tokens);
     r.block_m = tiles.block_m;
     r.block_n = tiles.block_n;
     r.threads = tiles.threads;
@@ -902,7 +904,7 @@ int ofh_attention_launch_info(const ofh_attention_params* p, ofh_launch_info* in
         info->merge_in_launch = merge_in_launch(p, r) ? 1 : 0;
         name = (p->dtype == OFH_DTYPE_F32 && (r.block_m == ofh::kRowsF32 || r.block_m == ofh::kRowsF32Narrow))
                    ? rows32_kernel_name(r.kdim, r.general_mod, r.block_m == ofh::kRowsF32Narrow)
-                   : ofh::flash_mfma_kernel_name(p->dtype, r.kdim, r.general_mod, r.tile_list);
+                   : ofh::flash_mfma_kernel_name(p->dtype, r.kdim, r.general_mod, r.tile_list, r.threads);
         // 16-bit causal pairs with a key split run the same tiling in a kernel of their own
         static thread_local std::string pair_name;
         const std::string lockstep = "flash_fwd_lockstep_kernel";

@@ -2210,7 +2210,16 @@ hipError_t launch(K kernel, int threads, const FwdArgs& a, hipStream_t s, bool p
 
 // 16-bit kernel workgroups: 8 wavefronts (256 query rows) without a
 // block-mask list, 4 wavefronts (128 rows, finer skipping) with one, and 4
-// wavefronts at D = 256 (register file).
+// wavefronts from D = 192 up (register file), except at D = 192 without
+// score_mod, where O (96 registers), Q (48) and a 64-key score tile fit two
+// wavefronts per SIMD: 8 wavefronts there whenever their workgroups fill the
+// CUs (B4 H32 N4096: 0.81 against 1.21 ms causal, 1.44 against 2.22 ms
+// non-causal, bit-identical), 4 on calls too small for that (whose 4-wavefront
+// grid or key split runs faster: bf16 causal B1 H8 N2048 43 against 59 us).
+static bool eight_waves_192(bool causal, int64_t bh, int64_t query_tokens) {
+    const int64_t nqt = (query_tokens + 255) / 256;
+    return bh * (causal ? (nqt + 1) / 2 : nqt) >= kComputeUnits;
+}
 
 // Causal calls without a block-mask list pair query tiles per workgroup.
 static bool pairs_causal_tiles(bool causal, bool tile_list) { return causal && !tile_list; }
@@ -2224,7 +2233,8 @@ static bool pairs_causal_tiles(bool causal, bool tile_list) { return causal && !
 // D = 32 stages 128 keys in every kernel without a block mask (a 64-key tile
 // of 64-byte rows is fewer 16-byte chunks than the 8 wavefronts copy), as do
 // D = 96 and 160 (their 64-key tiles do not split evenly over 512 threads);
-// D > 160 runs 4 wavefronts (128 query rows) on 64-key tiles throughout.
+// D > 160 runs 64-key tiles throughout, on 4 wavefronts (128 query rows) or,
+// at D = 192 without score_mod, 8.
 static int block_n16(int D, bool general_mod, bool tile_list) {
     if (D > 160 || tile_list) return kBlockN16;
     if (D == 32 || D == 96 || D == 160) return kBlockN16Wide;
@@ -2269,13 +2279,22 @@ static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
     }
     const bool pair_split = a.pair_split != 0;
     if constexpr (D > 160) {
-        if (pair_split)
-            return general_mod ? launch(flash_fwd_pair_split_kernel<T, D, MOD_GENERAL, 4>, 256, a, s, true)
-                               : launch(flash_fwd_pair_split_kernel<T, D, MOD_PLAIN, 4>, 256, a, s, true);
-        if (general_mod)
+        if (general_mod) {
+            if (pair_split) return launch(flash_fwd_pair_split_kernel<T, D, MOD_GENERAL, 4>, 256, a, s, true);
             return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 4, true>, 256, a, s, true)
                  : a.num_splits > 1 ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 4, false>, 256, a, s)
                           : launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 4, false, kBlockN16, 1, false>, 256, a, s);
+        }
+        if constexpr (D == 192) {  // 256-row query tiles: 8 wavefronts on 64-key tiles
+            // (chosen only where the workgroups fill the CUs, so never with a key split)
+            if (a.split_bm == 8 * kQueriesPerWave) {
+                if (pair_split || a.num_splits > 1) return hipErrorInvalidValue;
+                return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, true>, 512, a, s, true)
+                              : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, false, kBlockN16, 1, false>, 512, a, s);
+            }
+        }
+        if (a.split_bm != 4 * kQueriesPerWave) return hipErrorInvalidValue;
+        if (pair_split) return launch(flash_fwd_pair_split_kernel<T, D, MOD_PLAIN, 4>, 256, a, s, true);
         return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 4, true>, 256, a, s, true)
              : a.num_splits > 1 ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 4, false>, 256, a, s)
                       : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 4, false, kBlockN16, 1, false>, 256, a, s);
@@ -2419,43 +2438,49 @@ int flash_mfma_kernel_dim(int dtype, int D, int Dv) {
     return flash_mfma_head_dim(dtype, kd) ? kd : 0;
 }
 
-const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile_list) {
+const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile_list, int threads) {
     if (dtype < 0 || dtype > 2 || !flash_mfma_head_dim(dtype, D)) return "none";
-    // [dtype][D / 32 - 1][score_mod][list]
+    // [dtype][D / 32 - 1][score_mod][list][8 wavefronts]
     static const std::vector<std::string> names = [] {
         std::vector<std::string> v;
         const char* tn[3] = {"f32", "bf16", "f16"};
         for (int dt = 0; dt < 3; ++dt)
             for (int d = 32; d <= 256; d += 32)
                 for (int mod = 0; mod < 2; ++mod)
-                    for (int list = 0; list < 2; ++list) {
-                        std::string n;
-                        if (dt == DT_F32) {
-                            n = "flash_fwd_mfma32_kernel<" + std::to_string(d) + (mod ? ",general>" : ",plain>");
-                        } else {
-                            n = std::string("flash_fwd_lockstep_kernel<") + tn[dt] + "," + std::to_string(d) +
-                                (mod ? ",mod" : ",plain");
-                            const bool pow2 = (d & (d - 1)) == 0;
-                            if (list) n += ",list,4w>";
-                            else if (d > 160) n += ",4w>";
-                            else if (!mod && d <= 64) n += ",8w,128keys>";
-                            else if (!mod) n += ",8w,2x64keys>";
-                            else if (d == 32 || !pow2) n += ",8w,2x64keys>";
-                            else n += ",8w>";
+                    for (int list = 0; list < 2; ++list)
+                        for (int w8 = 0; w8 < 2; ++w8) {
+                            std::string n;
+                            if (dt == DT_F32) {
+                                n = "flash_fwd_mfma32_kernel<" + std::to_string(d) + (mod ? ",general>" : ",plain>");
+                            } else {
+                                n = std::string("flash_fwd_lockstep_kernel<") + tn[dt] + "," + std::to_string(d) +
+                                    (mod ? ",mod" : ",plain");
+                                const bool pow2 = (d & (d - 1)) == 0;
+                                if (list) n += ",list,4w>";
+                                else if (d == 192 && !mod && w8) n += ",8w>";
+                                else if (d > 160) n += ",4w>";
+                                else if (!mod && d <= 64) n += ",8w,128keys>";
+                                else if (!mod) n += ",8w,2x64keys>";
+                                else if (d == 32 || !pow2) n += ",8w,2x64keys>";
+                                else n += ",8w>";
+                            }
+                            v.push_back(n);
                         }
-                        v.push_back(n);
-                    }
         return v;
     }();
     const int di = D / 32 - 1;
-    return names[(((size_t)dtype * 8 + di) * 2 + (general_mod ? 1 : 0)) * 2 + (tile_list ? 1 : 0)].c_str();
+    return names[((((size_t)dtype * 8 + di) * 2 + (general_mod ? 1 : 0)) * 2 + (tile_list ? 1 : 0)) * 2 +
+                 (threads >= 512 ? 1 : 0)]
+        .c_str();
 }
 
-MfmaTiles flash_mfma_tiles(int dtype, int D, bool general_mod, bool tile_list, bool causal) {
+MfmaTiles flash_mfma_tiles(int dtype, int D, bool general_mod, bool tile_list, bool causal, int64_t bh,
+                           int64_t query_tokens) {
     if (dtype == DT_F32) return MfmaTiles{kBlockM32, kBlockNF32 * kTilesF32, kThreads32, false};
     const bool paired = pairs_causal_tiles(causal, tile_list);
     const int bn = block_n16(D, general_mod, tile_list);
-    if (tile_list || D > 160) return MfmaTiles{128, bn, 256, paired};
+    const bool four = tile_list || (D > 160 && !(D == 192 && !general_mod && eight_waves_192(causal, bh, query_tokens)));
+    if (four) return MfmaTiles{128, bn, 256, paired};
     return MfmaTiles{256, bn, 512, paired};
 }
 

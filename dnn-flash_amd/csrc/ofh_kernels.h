@@ -203,9 +203,16 @@ bool flash_mfma_head_dim(int dtype, int D);
 // need multiples of 8 up to 256, fp32 multiples of 4 up to 128 (16-byte row
 // chunks).
 int flash_mfma_kernel_dim(int dtype, int D, int Dv);
-const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile_list);
-// Workgroup tiling of the MFMA kernel for a dtype.
-MfmaTiles flash_mfma_tiles(int dtype, int head_dim, bool general_mod, bool tile_list, bool causal);
+// threads: the workgroup size of the tiling the call runs (flash_mfma_tiles).
+const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile_list, int threads);
+// Compute units of an MI355X.
+constexpr int kComputeUnits = 256;
+// Workgroup tiling of the MFMA kernel for a dtype and a call of bh heads
+// (batch x heads) and query_tokens rows: 16-bit D = 192 without score_mod or
+// block mask runs 8 wavefronts (256 rows) where their workgroups fill the
+// CUs, else 4 (128 rows).
+MfmaTiles flash_mfma_tiles(int dtype, int head_dim, bool general_mod, bool tile_list, bool causal, int64_t bh,
+                           int64_t query_tokens);
 
 // Scratch of the allocation-free entry point: a static device array of
 // kNoAllocScratchBytes per GPU. noalloc_scratch returns the current device's

@@ -203,6 +203,14 @@ def test_kernel_choice(ofh):
         (dict(dtype=F.DTYPE_BF16, head_dim=96), "flash_fwd_lockstep_kernel<bf16,96,plain,8w,2x64keys>"),
         (dict(dtype=F.DTYPE_F16, head_dim=160, softcap=5.0), "flash_fwd_lockstep_kernel<f16,160,mod,8w,2x64keys>"),
         (dict(dtype=F.DTYPE_BF16, head_dim=192), "flash_fwd_lockstep_kernel<bf16,192,plain,4w>"),
+        # D = 192 plain: 8 wavefronts where 256-row tiles (pairs when causal) fill the 256 CUs
+        (dict(dtype=F.DTYPE_BF16, head_dim=192, shape=(2, 64, 512, 512)), "flash_fwd_lockstep_kernel<bf16,192,plain,8w>"),
+        (dict(dtype=F.DTYPE_F16, head_dim=192, shape=(2, 128, 300, 512), causal=True),
+         "flash_fwd_lockstep_kernel<f16,192,plain,8w,paired>"),
+        (dict(dtype=F.DTYPE_F16, head_dim=192, shape=(2, 127, 300, 512), causal=True),
+         "flash_fwd_lockstep_kernel<f16,192,plain,4w,paired>"),
+        (dict(dtype=F.DTYPE_BF16, head_dim=192, shape=(2, 64, 512, 512), softcap=5.0),
+         "flash_fwd_lockstep_kernel<bf16,192,mod,4w>"),
         # head dims that are not a kernel's own: the kernel of max(D, Dv) rounded up to 32
         (dict(dtype=F.DTYPE_BF16, head_dim=80), "flash_fwd_lockstep_kernel<bf16,96,plain,8w,2x64keys>"),
         (dict(dtype=F.DTYPE_BF16, head_dim=64, value_dim=128), "flash_fwd_lockstep_kernel<bf16,128,plain,8w,2x64keys>"),
@@ -227,6 +235,12 @@ def test_kernel_choice(ofh):
     # causal: query tiles nqt-1-p and p share a workgroup
     assert info.workgroups == 4 * 32 * 8 and info.block_m == 256 and info.threads == 512
     assert info.key_splits == 1
+    info = F.launch_info(F.make_params(4, 32, 4096, 4096, 192, dtype=F.DTYPE_BF16, causal=True))
+    assert info.workgroups == 4 * 32 * 8 and info.block_m == 256 and info.threads == 512
+    assert info.key_splits == 1 and info.block_n == 64
+    # too few 256-row pairs to fill the CUs: 128-row tiles (which then split their keys)
+    info = F.launch_info(F.make_params(1, 8, 2048, 2048, 192, dtype=F.DTYPE_BF16, causal=True))
+    assert info.block_m == 128 and info.threads == 256 and info.key_splits > 1
     # 16-bit decode: 8 heads x 1 query tile -> 256 staged 128-key tiles per head
     # in 32 splits of 8: 256 workgroups, one round of the 256 CUs (one
     # 8-wavefront workgroup per CU)

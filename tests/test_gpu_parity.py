@@ -697,6 +697,38 @@ def test_rescale_with_score_mod(ofh, dt, splits):
         check(out, ref, dt, f"{dt} score_mod rescale causal={causal} max_key_splits={splits}")
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_d192_eight_wavefronts(ofh, dt):
+    """16-bit D = 192 without score_mod runs 8 wavefronts (256-row query
+    tiles, two per SIMD) where its workgroups fill the CUs, else 4 (128 rows,
+    checked against the oracle above). Heads are independent and a row's
+    arithmetic is the same in both, so the first heads of a 256-head call (8
+    wavefronts) equal the same heads run alone (4 wavefronts) bit for bit; two
+    of them are checked against the oracle as well. The rescale inputs (a
+    live-accumulator rescale), both signs of the scale, causal (query tile
+    pairs) and not."""
+    F = ofh
+    B, H, M, N, D = 2, 128, 300, 512, 192
+    code = {"bf16": F.DTYPE_BF16, "f16": F.DTYPE_F16}[dt]
+    for causal in (False, True):
+        big = F.launch_info(F.make_params(B, H, M, N, D, dtype=code, causal=causal)).kernel_name.decode()
+        small = F.launch_info(F.make_params(1, 2, M, N, D, dtype=code, causal=causal)).kernel_name.decode()
+        assert ",8w" in big and ",4w" in small, (big, small)
+    for sign in (1.0, -1.0):
+        dev, host, scale = rescale_inputs(dt, B, H, M, N, D, seed=11 + int(sign > 0), sign=sign)
+        for causal in (False, True):
+            out = run(ofh, dev, dt=dt, causal=causal, scale=scale, max_key_splits=1)
+            assert np.isfinite(out).all()
+            # the first two heads of the grid and the last two
+            for b, hs in ((0, slice(0, 2)), (B - 1, slice(H - 2, H))):
+                sub = tuple(t[b:b + 1, hs].contiguous() for t in dev)
+                alone = run(ofh, sub, dt=dt, causal=causal, scale=scale, max_key_splits=1)
+                label = f"{dt} D192 8 wavefronts causal={causal} scale={scale:+.4f} batch {b} heads {hs}"
+                assert np.array_equal(out[b:b + 1, hs], alone), f"{label}: heads differ from the 4-wavefront call"
+                ref = oracle_full(tuple(h[b:b + 1, hs] for h in host), causal=causal, scale=scale)
+                check(out[b:b + 1, hs], ref, dt, label)
+
+
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
 @pytest.mark.parametrize("D", [32, 96, 160, 192, 224, 256])
 def test_head_dims_beyond_64_and_128(ofh, dt, D):
