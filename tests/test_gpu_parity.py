@@ -706,7 +706,7 @@ def test_d192_eight_wavefronts(ofh, dt):
     wavefronts) equal the same heads run alone (4 wavefronts) bit for bit; two
     of them are checked against the oracle as well. The rescale inputs (a
     live-accumulator rescale), both signs of the scale, causal (query tile
-    pairs) and not."""
+    pairs) and not; then D != Dv calls that this kernel serves."""
     F = ofh
     B, H, M, N, D = 2, 128, 300, 512, 192
     code = {"bf16": F.DTYPE_BF16, "f16": F.DTYPE_F16}[dt]
@@ -727,6 +727,19 @@ def test_d192_eight_wavefronts(ofh, dt):
                 assert np.array_equal(out[b:b + 1, hs], alone), f"{label}: heads differ from the 4-wavefront call"
                 ref = oracle_full(tuple(h[b:b + 1, hs] for h in host), causal=causal, scale=scale)
                 check(out[b:b + 1, hs], ref, dt, label)
+    # head dims served by the D = 192 kernel: D = 192 with Dv = 128 (ragged key tiles), D = 160 with Dv = 192
+    for Dq, Dv, N2 in ((192, 128, 700), (160, 192, 333)):
+        assert ",8w" in F.launch_info(F.make_params(B, H, M, N2, Dq, Dv, dtype=code)).kernel_name.decode()
+        dev, host = make_inputs(dt, B, H, M, N2, Dq, Dv, seed=Dq + Dv)
+        for causal in (False, True):
+            out = run(ofh, dev, dt=dt, causal=causal, max_key_splits=1)
+            assert np.isfinite(out).all() and out.shape[-1] == Dv
+            for b, hs in ((0, slice(0, 2)), (B - 1, slice(H - 2, H))):
+                sub = tuple(t[b:b + 1, hs].contiguous() for t in dev)
+                alone = run(ofh, sub, dt=dt, causal=causal, max_key_splits=1)
+                label = f"{dt} D{Dq} Dv{Dv} N{N2} 8 wavefronts causal={causal} batch {b} heads {hs}"
+                assert np.array_equal(out[b:b + 1, hs], alone), f"{label}: heads differ from the 4-wavefront call"
+                check(out[b:b + 1, hs], oracle_full(tuple(h[b:b + 1, hs] for h in host), causal=causal), dt, label)
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
