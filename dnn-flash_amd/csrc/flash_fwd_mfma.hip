@@ -2210,13 +2210,16 @@ hipError_t launch(K kernel, int threads, const FwdArgs& a, hipStream_t s, bool p
 
 // 16-bit kernel workgroups: 8 wavefronts (256 query rows) without a
 // block-mask list, 4 wavefronts (128 rows, finer skipping) with one, and 4
-// wavefronts from D = 192 up (register file), except at D = 192 without
-// score_mod, where O (96 registers), Q (48) and a 64-key score tile fit two
-// wavefronts per SIMD: 8 wavefronts there whenever their workgroups fill the
-// CUs (B4 H32 N4096: 0.81 against 1.21 ms causal, 1.44 against 2.22 ms
-// non-causal, bit-identical), 4 on calls too small for that (whose 4-wavefront
-// grid or key split runs faster: bf16 causal B1 H8 N2048 43 against 59 us).
-static bool eight_waves_192(bool causal, int64_t bh, int64_t query_tokens) {
+// wavefronts from D = 192 up (register file), except without score_mod at
+// D = 192, where O (96 registers), Q (48) and a 64-key score tile fit two
+// wavefronts per SIMD, and at D = 256 with 32-key compute steps (64 keys
+// staged; 34-54 VGPRs spilled): 8 wavefronts there whenever their workgroups
+// fill the CUs (B4 H32 N4096, D = 192: 0.81 against 1.21 ms causal, 1.44
+// against 2.22 ms non-causal, bit-identical; D = 256: 1.41 against 1.45 ms
+// causal, 2.59 against 2.82 ms non-causal), 4 on calls too small for that
+// (whose 4-wavefront grid or key split runs faster: bf16 causal B1 H8 N2048
+// D192 43 against 59 us).
+static bool eight_waves_wide(bool causal, int64_t bh, int64_t query_tokens) {
     const int64_t nqt = (query_tokens + 255) / 256;
     return bh * (causal ? (nqt + 1) / 2 : nqt) >= kComputeUnits;
 }
@@ -2234,7 +2237,8 @@ static bool pairs_causal_tiles(bool causal, bool tile_list) { return causal && !
 // of 64-byte rows is fewer 16-byte chunks than the 8 wavefronts copy), as do
 // D = 96 and 160 (their 64-key tiles do not split evenly over 512 threads);
 // D > 160 runs 64-key tiles throughout, on 4 wavefronts (128 query rows) or,
-// at D = 192 without score_mod, 8.
+// at D = 192 and 256 without score_mod, 8 (two 32-key compute steps per
+// staged tile at D = 256).
 static int block_n16(int D, bool general_mod, bool tile_list) {
     if (D > 160 || tile_list) return kBlockN16;
     if (D == 32 || D == 96 || D == 160) return kBlockN16Wide;
@@ -2284,6 +2288,13 @@ static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
             return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 4, true>, 256, a, s, true)
                  : a.num_splits > 1 ? launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 4, false>, 256, a, s)
                           : launch(flash_fwd_lockstep_kernel<T, D, MOD_GENERAL, false, 4, false, kBlockN16, 1, false>, 256, a, s);
+        }
+        if constexpr (D == 256) {  // 256-row query tiles: 8 wavefronts, 64 keys staged as two 32-key steps
+            if (a.split_bm == 8 * kQueriesPerWave) {
+                if (pair_split || a.num_splits > 1) return hipErrorInvalidValue;
+                return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, true, 32, 2>, 512, a, s, true)
+                              : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, false, 32, 2, false>, 512, a, s);
+            }
         }
         if constexpr (D == 192) {  // 256-row query tiles: 8 wavefronts on 64-key tiles
             // (chosen only where the workgroups fill the CUs, so never with a key split)
@@ -2458,6 +2469,7 @@ const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile
                                 const bool pow2 = (d & (d - 1)) == 0;
                                 if (list) n += ",list,4w>";
                                 else if (d == 192 && !mod && w8) n += ",8w>";
+                                else if (d == 256 && !mod && w8) n += ",8w,2x32keys>";
                                 else if (d > 160) n += ",4w>";
                                 else if (!mod && d <= 64) n += ",8w,128keys>";
                                 else if (!mod) n += ",8w,2x64keys>";
@@ -2479,7 +2491,8 @@ MfmaTiles flash_mfma_tiles(int dtype, int D, bool general_mod, bool tile_list, b
     if (dtype == DT_F32) return MfmaTiles{kBlockM32, kBlockNF32 * kTilesF32, kThreads32, false};
     const bool paired = pairs_causal_tiles(causal, tile_list);
     const int bn = block_n16(D, general_mod, tile_list);
-    const bool four = tile_list || (D > 160 && !(D == 192 && !general_mod && eight_waves_192(causal, bh, query_tokens)));
+    const bool four =
+        tile_list || (D > 160 && !((D == 192 || D == 256) && !general_mod && eight_waves_wide(causal, bh, query_tokens)));
     if (four) return MfmaTiles{128, bn, 256, paired};
     return MfmaTiles{256, bn, 512, paired};
 }

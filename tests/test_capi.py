@@ -211,6 +211,12 @@ def test_kernel_choice(ofh):
          "flash_fwd_lockstep_kernel<f16,192,plain,4w,paired>"),
         (dict(dtype=F.DTYPE_BF16, head_dim=192, shape=(2, 64, 512, 512), softcap=5.0),
          "flash_fwd_lockstep_kernel<bf16,192,mod,4w>"),
+        (dict(dtype=F.DTYPE_BF16, head_dim=256, shape=(2, 64, 512, 512)),
+         "flash_fwd_lockstep_kernel<bf16,256,plain,8w,2x32keys>"),
+        (dict(dtype=F.DTYPE_F16, head_dim=256, shape=(2, 128, 300, 512), causal=True),
+         "flash_fwd_lockstep_kernel<f16,256,plain,8w,2x32keys,paired>"),
+        (dict(dtype=F.DTYPE_F16, head_dim=256, shape=(2, 64, 512, 512), softcap=5.0),
+         "flash_fwd_lockstep_kernel<f16,256,mod,4w>"),
         # head dims that are not a kernel's own: the kernel of max(D, Dv) rounded up to 32
         (dict(dtype=F.DTYPE_BF16, head_dim=80), "flash_fwd_lockstep_kernel<bf16,96,plain,8w,2x64keys>"),
         (dict(dtype=F.DTYPE_BF16, head_dim=64, value_dim=128), "flash_fwd_lockstep_kernel<bf16,128,plain,8w,2x64keys>"),

@@ -698,17 +698,19 @@ def test_rescale_with_score_mod(ofh, dt, splits):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
-def test_d192_eight_wavefronts(ofh, dt):
-    """16-bit D = 192 without score_mod runs 8 wavefronts (256-row query
-    tiles, two per SIMD) where its workgroups fill the CUs, else 4 (128 rows,
-    checked against the oracle above). Heads are independent and a row's
-    arithmetic is the same in both, so the first heads of a 256-head call (8
-    wavefronts) equal the same heads run alone (4 wavefronts) bit for bit; two
-    of them are checked against the oracle as well. The rescale inputs (a
-    live-accumulator rescale), both signs of the scale, causal (query tile
-    pairs) and not; then D != Dv calls that this kernel serves."""
+@pytest.mark.parametrize("D", [192, 256])
+def test_eight_wavefronts_wide_head_dims(ofh, dt, D):
+    """16-bit D = 192 and 256 without score_mod run 8 wavefronts (256-row
+    query tiles, two per SIMD) where their workgroups fill the CUs, else 4
+    (128 rows, checked against the oracle above). Heads are independent: the
+    first and last heads of a 256-head call (8 wavefronts) are run alone as
+    well (4 wavefronts) and both are checked against the oracle; at D = 192 a
+    row's arithmetic is the same in both, so they agree bit for bit (D = 256
+    computes 32-key steps on 8 wavefronts, 64-key steps on 4). The rescale
+    inputs (a live-accumulator rescale), both signs of the scale, causal
+    (query tile pairs) and not; then D != Dv calls that the kernel serves."""
     F = ofh
-    B, H, M, N, D = 2, 128, 300, 512, 192
+    B, H, M, N = 2, 128, 300, 512
     code = {"bf16": F.DTYPE_BF16, "f16": F.DTYPE_F16}[dt]
     for causal in (False, True):
         big = F.launch_info(F.make_params(B, H, M, N, D, dtype=code, causal=causal)).kernel_name.decode()
@@ -723,12 +725,14 @@ def test_d192_eight_wavefronts(ofh, dt):
             for b, hs in ((0, slice(0, 2)), (B - 1, slice(H - 2, H))):
                 sub = tuple(t[b:b + 1, hs].contiguous() for t in dev)
                 alone = run(ofh, sub, dt=dt, causal=causal, scale=scale, max_key_splits=1)
-                label = f"{dt} D192 8 wavefronts causal={causal} scale={scale:+.4f} batch {b} heads {hs}"
-                assert np.array_equal(out[b:b + 1, hs], alone), f"{label}: heads differ from the 4-wavefront call"
+                label = f"{dt} D{D} 8 wavefronts causal={causal} scale={scale:+.4f} batch {b} heads {hs}"
                 ref = oracle_full(tuple(h[b:b + 1, hs] for h in host), causal=causal, scale=scale)
                 check(out[b:b + 1, hs], ref, dt, label)
-    # head dims served by the D = 192 kernel: D = 192 with Dv = 128 (ragged key tiles), D = 160 with Dv = 192
-    for Dq, Dv, N2 in ((192, 128, 700), (160, 192, 333)):
+                check(alone, ref, dt, label + " (4 wavefronts)")
+                if D == 192:
+                    assert np.array_equal(out[b:b + 1, hs], alone), f"{label}: heads differ from the 4-wavefront call"
+    # head dims the kernel serves: D with Dv = 128 (ragged key tiles), and Dv = D with a smaller D
+    for Dq, Dv, N2 in {192: ((192, 128, 700), (160, 192, 333)), 256: ((256, 128, 700), (224, 256, 333))}[D]:
         assert ",8w" in F.launch_info(F.make_params(B, H, M, N2, Dq, Dv, dtype=code)).kernel_name.decode()
         dev, host = make_inputs(dt, B, H, M, N2, Dq, Dv, seed=Dq + Dv)
         for causal in (False, True):
@@ -738,8 +742,11 @@ def test_d192_eight_wavefronts(ofh, dt):
                 sub = tuple(t[b:b + 1, hs].contiguous() for t in dev)
                 alone = run(ofh, sub, dt=dt, causal=causal, max_key_splits=1)
                 label = f"{dt} D{Dq} Dv{Dv} N{N2} 8 wavefronts causal={causal} batch {b} heads {hs}"
-                assert np.array_equal(out[b:b + 1, hs], alone), f"{label}: heads differ from the 4-wavefront call"
-                check(out[b:b + 1, hs], oracle_full(tuple(h[b:b + 1, hs] for h in host), causal=causal), dt, label)
+                ref = oracle_full(tuple(h[b:b + 1, hs] for h in host), causal=causal)
+                check(out[b:b + 1, hs], ref, dt, label)
+                check(alone, ref, dt, label + " (4 wavefronts)")
+                if D == 192:
+                    assert np.array_equal(out[b:b + 1, hs], alone), f"{label}: heads differ from the 4-wavefront call"
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
