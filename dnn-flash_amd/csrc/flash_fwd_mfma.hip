@@ -2213,15 +2213,19 @@ hipError_t launch(K kernel, int threads, const FwdArgs& a, hipStream_t s, bool p
 // wavefronts from D = 192 up (register file), except without score_mod at
 // D = 192, where O (96 registers), Q (48) and a 64-key score tile fit two
 // wavefronts per SIMD, and at D = 256 with 32-key compute steps (64 keys
-// staged; 34-54 VGPRs spilled): 8 wavefronts there whenever their workgroups
-// fill the CUs (B4 H32 N4096, D = 192: 0.81 against 1.21 ms causal, 1.44
-// against 2.22 ms non-causal, bit-identical; D = 256: 1.41 against 1.45 ms
-// causal, 2.59 against 2.82 ms non-causal), 4 on calls too small for that
-// (whose 4-wavefront grid or key split runs faster: bf16 causal B1 H8 N2048
-// D192 43 against 59 us).
+// staged; 34-54 VGPRs spilled): 8 wavefronts there whenever the 4-wavefront
+// grid (one workgroup per CU) would take more than one round of the CUs (B4
+// H32 N4096, D = 192: 0.81 against 1.21 ms causal, 1.44 against 2.22 ms
+// non-causal, bit-identical; D = 256: 1.41 against 1.45 ms causal, 2.59
+// against 2.82 ms non-causal; bf16 B1 H24 N2048 D192 non-causal, 192
+// workgroups of 8 against 384 of 4: 80 against 141 us), 4 on calls that one
+// round holds (whose 4-wavefront grid or key split runs faster: bf16 causal
+// B2 H16 N2048 D192 84 against 99 us with 8 wavefronts and a pair split, B1
+// H8 N2048 43 against 59 us). The 8-wavefront grid then never takes a key
+// split: it has more than half as many workgroups as CUs.
 static bool eight_waves_wide(bool causal, int64_t bh, int64_t query_tokens) {
-    const int64_t nqt = (query_tokens + 255) / 256;
-    return bh * (causal ? (nqt + 1) / 2 : nqt) >= kComputeUnits;
+    const int64_t nqt4 = (query_tokens + 127) / 128;
+    return bh * (causal ? (nqt4 + 1) / 2 : nqt4) > kComputeUnits;
 }
 
 // Causal calls without a block-mask list pair query tiles per workgroup.
@@ -2297,7 +2301,7 @@ static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
             }
         }
         if constexpr (D == 192) {  // 256-row query tiles: 8 wavefronts on 64-key tiles
-            // (chosen only where the workgroups fill the CUs, so never with a key split)
+            // (chosen only where its workgroups outnumber half the CUs, so never with a key split)
             if (a.split_bm == 8 * kQueriesPerWave) {
                 if (pair_split || a.num_splits > 1) return hipErrorInvalidValue;
                 return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, true>, 512, a, s, true)

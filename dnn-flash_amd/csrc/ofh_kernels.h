@@ -209,8 +209,8 @@ const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile
 constexpr int kComputeUnits = 256;
 // Workgroup tiling of the MFMA kernel for a dtype and a call of bh heads
 // (batch x heads) and query_tokens rows: 16-bit D = 192 and 256 without
-// score_mod or block mask run 8 wavefronts (256 rows) where their workgroups
-// fill the CUs, else 4 (128 rows).
+// score_mod or block mask run 8 wavefronts (256 rows) where 4 (128 rows, one
+// workgroup per CU) would take more than one round of the CUs, else 4.
 MfmaTiles flash_mfma_tiles(int dtype, int head_dim, bool general_mod, bool tile_list, bool causal, int64_t bh,
                            int64_t query_tokens);
 

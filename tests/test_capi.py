@@ -168,6 +168,30 @@ def test_null_pointers_rejected_before_any_device_work(ofh):
     assert "pointers must be non-null" in F.lib().ofh_last_error().decode()
 
 
+def test_eight_wavefront_wide_head_dims_never_split(ofh):
+    """16-bit D = 192 / 256 calls on 8 wavefronts (their launchers have no
+    key-split instantiation) are planned without a key split, over a sweep of
+    shapes around the point where the 4-wavefront grid outgrows one round of
+    the CUs; below it they run 4 wavefronts."""
+    F = ofh
+    seen = set()
+    for D in (192, 256):
+        for causal in (False, True):
+            for B, H in ((1, 8), (1, 16), (1, 17), (1, 24), (2, 16), (1, 33), (3, 11), (1, 128), (4, 32)):
+                for M in (1, 100, 256, 300, 1000, 2048, 2049, 4096):
+                    for dt in (F.DTYPE_BF16, F.DTYPE_F16):
+                        info = F.launch_info(F.make_params(B, H, M, max(M, 512), D, dtype=dt, causal=causal))
+                        nqt4 = -(-M // 128)
+                        wide = B * H * ((nqt4 + 1) // 2 if causal else nqt4) > 256
+                        name = info.kernel_name.decode()
+                        assert (",8w" in name) == wide, (D, causal, B, H, M, name)
+                        assert info.threads == (512 if wide else 256)
+                        if wide:
+                            assert info.key_splits == 1 and info.block_m == 256, (D, causal, B, H, M)
+                        seen.add(wide)
+    assert seen == {False, True}
+
+
 def test_kernel_choice(ofh):
     F = ofh
     cases = [
@@ -203,11 +227,14 @@ def test_kernel_choice(ofh):
         (dict(dtype=F.DTYPE_BF16, head_dim=96), "flash_fwd_lockstep_kernel<bf16,96,plain,8w,2x64keys>"),
         (dict(dtype=F.DTYPE_F16, head_dim=160, softcap=5.0), "flash_fwd_lockstep_kernel<f16,160,mod,8w,2x64keys>"),
         (dict(dtype=F.DTYPE_BF16, head_dim=192), "flash_fwd_lockstep_kernel<bf16,192,plain,4w>"),
-        # D = 192 plain: 8 wavefronts where 256-row tiles (pairs when causal) fill the 256 CUs
+        # D = 192 plain: 8 wavefronts where 128-row tiles (pairs when causal) would take more than one
+        # round of the 256 CUs
         (dict(dtype=F.DTYPE_BF16, head_dim=192, shape=(2, 64, 512, 512)), "flash_fwd_lockstep_kernel<bf16,192,plain,8w>"),
+        (dict(dtype=F.DTYPE_BF16, head_dim=192, shape=(1, 24, 2048, 2048)), "flash_fwd_lockstep_kernel<bf16,192,plain,8w>"),
+        (dict(dtype=F.DTYPE_BF16, head_dim=192, shape=(1, 16, 2048, 2048)), "flash_fwd_lockstep_kernel<bf16,192,plain,4w>"),
         (dict(dtype=F.DTYPE_F16, head_dim=192, shape=(2, 128, 300, 512), causal=True),
          "flash_fwd_lockstep_kernel<f16,192,plain,8w,paired>"),
-        (dict(dtype=F.DTYPE_F16, head_dim=192, shape=(2, 127, 300, 512), causal=True),
+        (dict(dtype=F.DTYPE_F16, head_dim=192, shape=(2, 16, 2048, 2048), causal=True),
          "flash_fwd_lockstep_kernel<f16,192,plain,4w,paired>"),
         (dict(dtype=F.DTYPE_BF16, head_dim=192, shape=(2, 64, 512, 512), softcap=5.0),
          "flash_fwd_lockstep_kernel<bf16,192,mod,4w>"),
@@ -244,7 +271,7 @@ def test_kernel_choice(ofh):
     info = F.launch_info(F.make_params(4, 32, 4096, 4096, 192, dtype=F.DTYPE_BF16, causal=True))
     assert info.workgroups == 4 * 32 * 8 and info.block_m == 256 and info.threads == 512
     assert info.key_splits == 1 and info.block_n == 64
-    # too few 256-row pairs to fill the CUs: 128-row tiles (which then split their keys)
+    # one round of 128-row pairs or fewer: 128-row tiles (which then split their keys)
     info = F.launch_info(F.make_params(1, 8, 2048, 2048, 192, dtype=F.DTYPE_BF16, causal=True))
     assert info.block_m == 128 and info.threads == 256 and info.key_splits > 1
     # 16-bit decode: 8 heads x 1 query tile -> 256 staged 128-key tiles per head
