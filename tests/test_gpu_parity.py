@@ -296,6 +296,28 @@ def test_strided_layouts(ofh):
     check(out.cpu().numpy(), oracle_full(host, causal=True), "bf16", "strided [B,T,H,D]")
 
 
+@pytest.mark.parametrize("D", [192, 256])
+def test_strided_layouts_eight_wavefronts(ofh, D):
+    """The 8-wavefront D = 192 / 256 kernels on [B,T,H,D] storage: the same
+    output, bit for bit, as on contiguous [B,H,T,D] copies of the inputs
+    (strides change only addresses), with bf16 output, causal and not; two
+    heads against the oracle."""
+    B, H, M, N = 2, 128, 300, 333
+    assert ",8w" in ofh.launch_info(ofh.make_params(B, H, M, N, D, dtype=ofh.DTYPE_BF16)).kernel_name.decode()
+    dev, host = make_inputs("bf16", B, H, M, N, D, seed=D + 3)
+    strided = tuple(t.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3) for t in dev)
+    for causal in (False, True):
+        ref_out = run(ofh, dev, dt="bf16", causal=causal, out_dtype="bf16")
+        out_store = torch.empty((B, M, H, D), device="cuda", dtype=torch.bfloat16)
+        out = out_store.permute(0, 2, 1, 3)
+        ofh.attention_fwd(*strided, causal=causal, out=out)
+        torch.cuda.synchronize()
+        got = out.float().cpu().numpy()
+        assert np.array_equal(got, ref_out), f"D{D} causal={causal}: strided output differs"
+        check(got[:1, :2], oracle_full(tuple(h[:1, :2] for h in host), causal=causal), "bf16",
+              f"strided [B,T,H,D] D{D} 8 wavefronts causal={causal}", out_dt="bf16")
+
+
 def test_output_dtypes_and_determinism(ofh):
     dev, host = make_inputs("bf16", 1, 4, 256, 256, 128, seed=14)
     a = run(ofh, dev, dt="bf16", causal=True, out_dtype="bf16")
