@@ -912,6 +912,13 @@ int ofh_attention_launch_info(const ofh_attention_params* p, ofh_launch_info* in
             pair_name = "flash_fwd_pair_split_kernel" + std::string(name).substr(lockstep.size());
             name = pair_name.c_str();
         }
+        // 16-bit D = 192 on 8 wavefronts with value_dim <= 128: PV over 128 value columns only
+        if (p->dtype != OFH_DTYPE_F32 && r.kdim == 192 && r.threads >= 512 && p->value_dim <= 128 &&
+            std::string(name).compare(0, lockstep.size(), lockstep) == 0) {
+            pair_name = std::string(name);
+            pair_name.insert(pair_name.size() - 1, ",v128");
+            name = pair_name.c_str();
+        }
         // 16-bit causal query tiles run in pairs per workgroup (nqt-1-p, p)
         if (r.paired && !r.pair_split && p->dtype != OFH_DTYPE_F32 &&
             std::string(name).compare(0, lockstep.size(), lockstep) == 0) {

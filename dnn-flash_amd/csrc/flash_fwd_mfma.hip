@@ -551,8 +551,11 @@ __device__ __forceinline__ constexpr int tile_pos(int sb, int e) { return 32 * s
 // The per-wavefront state and the tile operations of one 32-row wavefront.
 // A "tile step" is identified by its entry: the key tile index, or with a
 // block-mask list (LIST) the list entry (key tile + per-slice bits).
-template <typename T, int D, int MOD, bool LIST, int NTHREADS, int BN_, int SB = 1>
+template <typename T, int D, int MOD, bool LIST, int NTHREADS, int BN_, int SB = 1, int DVK = D>
 struct Wave32 {
+    // DVK: value columns the kernel computes (a multiple of 32 up to D; O and
+    // PV cover only those, the K side and the LDS rows stay D wide)
+    static_assert(DVK % 32 == 0 && DVK <= D, "value columns: a multiple of 32 up to D");
     using T_ = T;
     using M16 = Mfma16<T>;
     using v8 = typename M16::v8;
@@ -573,7 +576,7 @@ struct Wave32 {
     int ntiles;
     const int* list;
     v8 qf[D / 16];
-    f32x16 o[D / 32];
+    f32x16 o[DVK / 32];
     f32x16 s[BN / 32];
     v8 pf[BN / 16];
     float m_run, l_run;
@@ -634,7 +637,7 @@ struct Wave32 {
             qf[c] = __builtin_bit_cast(v8, u);
         }
 #pragma unroll
-        for (int db = 0; db < D / 32; ++db) o[db] = f32x16{};
+        for (int db = 0; db < DVK / 32; ++db) o[db] = f32x16{};
         m_run = kNegInf;
         l_run = 0.0f;
         slope = 0.0f;
@@ -782,7 +785,7 @@ struct Wave32 {
             return __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         };
         // V^T fragments kFragAhead MFMAs ahead (see qk)
-        constexpr int NF = (D / 32) * (BN / 16);
+        constexpr int NF = (DVK / 32) * (BN / 16);
         v8 f[kFragAhead];
 #pragma unroll
         for (int i = 0; i < kFragAhead; ++i) f[i] = vfrag(i % (BN / 16), i / (BN / 16));
@@ -981,7 +984,7 @@ struct Wave32 {
             m_run = raise ? mx : m_run;
             l_run *= alpha;
 #pragma unroll
-            for (int db = 0; db < D / 32; ++db) o[db] *= alpha;
+            for (int db = 0; db < DVK / 32; ++db) o[db] *= alpha;
         }
         const float m_use = (m_run == kNegInf) ? 0.0f : m_run;
 
@@ -1023,7 +1026,7 @@ struct Wave32 {
         float* po = a.part_o + prow * a.Dv + 8 * g;
         const bool coh = a.split_counters != nullptr;
 #pragma unroll
-        for (int db = 0; db < D / 32; ++db) {
+        for (int db = 0; db < DVK / 32; ++db) {
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) {
                 if (32 * db + 16 * cc + 8 * g >= a.Dv) continue;  // past the value dim
@@ -1051,7 +1054,7 @@ struct Wave32 {
         if (a.out_f32) {
             float* orow = (float*)a.o + b * a.o_sb + h * a.o_sh + (int64_t)my_q * a.o_sm + 8 * g;
 #pragma unroll
-            for (int db = 0; db < D / 32; ++db) {
+            for (int db = 0; db < DVK / 32; ++db) {
 #pragma unroll
                 for (int cc = 0; cc < 2; ++cc) {
                     if (32 * db + 16 * cc + 8 * g >= a.Dv) continue;  // past the value dim
@@ -1068,7 +1071,7 @@ struct Wave32 {
         } else {
             T* orow = (T*)a.o + b * a.o_sb + h * a.o_sh + (int64_t)my_q * a.o_sm + 8 * g;
 #pragma unroll
-            for (int db = 0; db < D / 32; ++db) {
+            for (int db = 0; db < DVK / 32; ++db) {
 #pragma unroll
                 for (int cc = 0; cc < 2; ++cc) {
                     if (32 * db + 16 * cc + 8 * g >= a.Dv) continue;  // past the value dim
@@ -1270,13 +1273,13 @@ __device__ __forceinline__ void lds_list_qtile(const FwdArgs& a, unsigned char* 
     w.store_output();
 }
 
-template <typename T, int D, int MOD, bool LIST, int NWAVES, int BN, int SB, bool SPLIT>
+template <typename T, int D, int MOD, bool LIST, int NWAVES, int BN, int SB, bool SPLIT, int DVK = D>
 __device__ __forceinline__ void lockstep_qtile(const FwdArgs& a, unsigned char* smem, int bh, int qt,
                                                int split = 0) {
     constexpr int NTHREADS = NWAVES * 64;
     constexpr int BLOCK_M = NWAVES * kQueriesPerWave;
     static_assert(!LIST || NWAVES <= kListSlices, "list entries carry one bit per wavefront");
-    using W = Wave32<T, D, MOD, LIST, NTHREADS, BN, SB>;
+    using W = Wave32<T, D, MOD, LIST, NTHREADS, BN, SB, DVK>;
     using L = typename W::L;
     static_assert(2 * L::STAGE >= 24 * NTHREADS + 4, "split merge scratch fits in the LDS stages");
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1402,7 +1405,7 @@ constexpr int lockstep_min_blocks(int D, int nwaves, int mod, bool list) {
 // one split take the instantiation without it, whose loop then keeps the
 // split's values out of its scalar registers (fewer spilled to vector lanes).
 template <typename T, int D, int MOD, bool LIST, int NWAVES, bool PAIRED, int BN = kBlockN16, int SB = 1,
-          bool SPLIT = true>
+          bool SPLIT = true, int DVK = D>
 __global__ __launch_bounds__(NWAVES * 64, lockstep_min_blocks(D, NWAVES, MOD, LIST)) void flash_fwd_lockstep_kernel(FwdArgs a) {
     using L = TileLayout<D, BN * SB>;
     // block-mask kernels: LDS sized at launch (list_kernel_lds_bytes)
@@ -1414,15 +1417,15 @@ __global__ __launch_bounds__(NWAVES * 64, lockstep_min_blocks(D, NWAVES, MOD, LI
         const int tiles = a.B * a.H * a.num_q_tiles;
         const int split = (int)blockIdx.x / tiles;
         map_work((int)blockIdx.x - split * tiles, a.B * a.H, a.num_q_tiles, a.causal, bh, qts[0]);
-        lockstep_qtile<T, D, MOD, LIST, NWAVES, BN, SB, SPLIT>(a, smem, bh, qts[0], split);
+        lockstep_qtile<T, D, MOD, LIST, NWAVES, BN, SB, SPLIT, DVK>(a, smem, bh, qts[0], split);
         return;
     }
     // (paired query tiles are never split)
     const int n = work_tiles(a, PAIRED, bh, qts);
-    lockstep_qtile<T, D, MOD, LIST, NWAVES, BN, SB, false>(a, smem, bh, qts[0]);
+    lockstep_qtile<T, D, MOD, LIST, NWAVES, BN, SB, false, DVK>(a, smem, bh, qts[0]);
     if (n > 1) {
         __syncthreads();  // LDS stages are reused
-        lockstep_qtile<T, D, MOD, LIST, NWAVES, BN, SB, false>(a, smem, bh, qts[1]);
+        lockstep_qtile<T, D, MOD, LIST, NWAVES, BN, SB, false, DVK>(a, smem, bh, qts[1]);
     }
 }
 
@@ -2304,6 +2307,9 @@ static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
             // (chosen only where its workgroups outnumber half the CUs, so never with a key split)
             if (a.split_bm == 8 * kQueriesPerWave) {
                 if (pair_split || a.num_splits > 1) return hipErrorInvalidValue;
+                if (a.Dv <= 128)  // value columns 128 (e.g. 192/128 query-key/value heads): PV over those only
+                    return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, true, kBlockN16, 1, true, 128>, 512, a, s, true)
+                                  : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, false, kBlockN16, 1, false, 128>, 512, a, s);
                 return paired ? launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, true>, 512, a, s, true)
                               : launch(flash_fwd_lockstep_kernel<T, D, MOD_PLAIN, false, 8, false, kBlockN16, 1, false>, 512, a, s);
             }

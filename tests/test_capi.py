@@ -232,6 +232,13 @@ def test_kernel_choice(ofh):
         (dict(dtype=F.DTYPE_BF16, head_dim=192, shape=(2, 64, 512, 512)), "flash_fwd_lockstep_kernel<bf16,192,plain,8w>"),
         (dict(dtype=F.DTYPE_BF16, head_dim=192, shape=(1, 24, 2048, 2048)), "flash_fwd_lockstep_kernel<bf16,192,plain,8w>"),
         (dict(dtype=F.DTYPE_BF16, head_dim=192, shape=(1, 16, 2048, 2048)), "flash_fwd_lockstep_kernel<bf16,192,plain,4w>"),
+        # 192/128 query-key/value heads: PV over the 128 value columns only
+        (dict(dtype=F.DTYPE_BF16, head_dim=192, value_dim=128, shape=(1, 128, 4096, 4096), causal=True),
+         "flash_fwd_lockstep_kernel<bf16,192,plain,8w,v128,paired>"),
+        (dict(dtype=F.DTYPE_F16, head_dim=192, value_dim=96, shape=(1, 128, 4096, 4096)),
+         "flash_fwd_lockstep_kernel<f16,192,plain,8w,v128>"),
+        (dict(dtype=F.DTYPE_F16, head_dim=192, value_dim=160, shape=(1, 128, 4096, 4096)),
+         "flash_fwd_lockstep_kernel<f16,192,plain,8w>"),
         (dict(dtype=F.DTYPE_F16, head_dim=192, shape=(2, 128, 300, 512), causal=True),
          "flash_fwd_lockstep_kernel<f16,192,plain,8w,paired>"),
         (dict(dtype=F.DTYPE_F16, head_dim=192, shape=(2, 16, 2048, 2048), causal=True),

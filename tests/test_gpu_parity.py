@@ -754,7 +754,9 @@ def test_eight_wavefronts_wide_head_dims(ofh, dt, D):
                 if D == 192:
                     assert np.array_equal(out[b:b + 1, hs], alone), f"{label}: heads differ from the 4-wavefront call"
     # head dims the kernel serves: D with Dv = 128 (ragged key tiles), and Dv = D with a smaller D
-    for Dq, Dv, N2 in {192: ((192, 128, 700), (160, 192, 333)), 256: ((256, 128, 700), (224, 256, 333))}[D]:
+    # (at D = 192, value dims up to 128 run PV over 128 columns only)
+    for Dq, Dv, N2 in {192: ((192, 128, 700), (160, 192, 333), (192, 96, 512)),
+                       256: ((256, 128, 700), (224, 256, 333))}[D]:
         assert ",8w" in F.launch_info(F.make_params(B, H, M, N2, Dq, Dv, dtype=code)).kernel_name.decode()
         dev, host = make_inputs(dt, B, H, M, N2, Dq, Dv, seed=Dq + Dv)
         for causal in (False, True):
