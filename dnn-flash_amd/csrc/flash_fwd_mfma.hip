@@ -581,6 +581,7 @@ struct Wave32 {
     v8 pf[BN / 16];
     float m_run, l_run;
     float slope;
+    float alibi_step[8];  // soft-capped ALiBi: 2^(slope c_b t), t = 0..7 (wave-uniform)
     const float* bias_row;
     // LDS read lane offsets
     int k_lane_off, v_lane_off;
@@ -644,6 +645,11 @@ struct Wave32 {
         bias_row = nullptr;
         if (MOD == MOD_GENERAL) {
             if (a.bias_kind == BIAS_ALIBI) slope = a.alibi[h];
+            const float sl8 = slope * (2.0f * kLog2e) * a.inv_softcap;
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+                alibi_step[t] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, __builtin_amdgcn_exp2f(sl8 * (float)t))));
             if (a.bias_kind == BIAS_DENSE)
                 bias_row = a.bias + b * a.bias_sb + h * a.bias_sh + (int64_t)min(my_q, a.M - 1) * a.bias_sm;
         }
@@ -831,6 +837,22 @@ struct Wave32 {
                     for (int e = 0; e < 16; ++e)
                         bvals[16 * sb + e] = bias_row[min(k0 + 8 * g + tile_pos(sb, e), a.N - 1)];
             }
+        }
+        if constexpr (BIAS == BIAS_ALIBI && CAP) {
+            // 2^u = 2^(c_s s + base_j) * 2^(sl t) with key 8-group base_j and t = key & 7: the ALiBi step
+            // inside a group rides on the "+ 1" of the soft-cap as a multiply-add
+#pragma unroll
+            for (int sb = 0; sb < BN / 32; ++sb)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const float bj = __builtin_fmaf(sl, (float)(32 * sb + 16 * hh), base);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        const float x = __builtin_amdgcn_exp2f(__builtin_fmaf(s[sb][8 * hh + t], c_s, bj));
+                        s[sb][8 * hh + t] = __builtin_amdgcn_rcpf(__builtin_fmaf(x, alibi_step[t], 1.0f));
+                    }
+                }
+            return;
         }
 #pragma unroll
         for (int sb = 0; sb < BN / 32; ++sb)
