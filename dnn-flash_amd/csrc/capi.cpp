@@ -285,8 +285,8 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
                          std::llabs((long long)r.ks[2]) <= (1 << 24) && std::llabs((long long)r.vs[2]) <= (1 << 24);
     if (p->algorithm == OFH_ALGO_FLASH_MFMA && !mfma_ok)
         return set_error(OFH_ERROR_UNSUPPORTED,
-                         "flash MFMA kernel needs head_dim and value_dim multiples of 4 up to 128 (fp32) "
-                         "or of 8 up to 256 (bf16/fp16), 16-byte "
+                         "flash MFMA kernel needs head_dim and value_dim multiples of 4 (fp32) "
+                         "or of 8 (bf16/fp16) up to 256, 16-byte "
                          "aligned rows and K/V token strides of at most 2^24 elements; use "
                          "OFH_ALGO_AUTO or OFH_ALGO_ROWWISE");
     if (p->algorithm == OFH_ALGO_ROWWISE || !mfma_ok) {
@@ -318,8 +318,8 @@ int resolve(const ofh_attention_params* p, const void* q, const void* k, const v
     r.num_k_tiles = (int)((p->key_tokens + r.block_n - 1) / r.block_n);
     r.tile_list = p->mask_allowed != nullptr;
     // fp32 with few query tiles (latency-bound): 32-row query blocks whose
-    // four wavefronts share the keys, 32-key tiles
-    if (p->dtype == OFH_DTYPE_F32 && !r.tile_list &&
+    // four wavefronts share the keys, 32-key tiles (built up to D = 128)
+    if (p->dtype == OFH_DTYPE_F32 && !r.tile_list && r.kdim <= 128 &&
         (int64_t)p->batch * p->heads * r.num_q_tiles < ofh::kRows32Below) {
         r.block_m = ofh::kRowsF32;
         r.block_n = 32;

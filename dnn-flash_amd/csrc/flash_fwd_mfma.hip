@@ -2360,14 +2360,17 @@ static hipError_t launch16(const FwdArgs& a, bool general_mod, hipStream_t s) {
 }
 
 // fp32 128-row query tiles: causal pairs without a block mask take the
-// pairs-only instantiation.
+// pairs-only instantiation. Above D = 128 a K/V tile is one block of 32 keys
+// (two stages of 64-key tiles would not fit the LDS).
 template <int D>
 static hipError_t launch32(const FwdArgs& a, bool general_mod, hipStream_t s) {
+    constexpr int NB = D > 128 ? 1 : kTilesF32;
+    if (a.split_bn != kBlockNF32 * NB) return hipErrorInvalidValue;
     if (a.pair_split && a.tile_counts == nullptr)
-        return general_mod ? launch(flash_fwd_mfma32_kernel<D, true, kTilesF32, true>, kThreads32, a, s, true)
-                           : launch(flash_fwd_mfma32_kernel<D, false, kTilesF32, true>, kThreads32, a, s, true);
-    return general_mod ? launch(flash_fwd_mfma32_kernel<D, true, kTilesF32>, kThreads32, a, s, a.pair_split != 0)
-                       : launch(flash_fwd_mfma32_kernel<D, false, kTilesF32>, kThreads32, a, s, a.pair_split != 0);
+        return general_mod ? launch(flash_fwd_mfma32_kernel<D, true, NB, true>, kThreads32, a, s, true)
+                           : launch(flash_fwd_mfma32_kernel<D, false, NB, true>, kThreads32, a, s, true);
+    return general_mod ? launch(flash_fwd_mfma32_kernel<D, true, NB>, kThreads32, a, s, a.pair_split != 0)
+                       : launch(flash_fwd_mfma32_kernel<D, false, NB>, kThreads32, a, s, a.pair_split != 0);
 }
 
 hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipStream_t s) {
@@ -2417,6 +2420,10 @@ hipError_t launch_flash_mfma(const FwdArgs& a, int dtype, bool general_mod, hipS
             case 64: return launch32<64>(a, general_mod, s);
             case 96: return launch32<96>(a, general_mod, s);
             case 128: return launch32<128>(a, general_mod, s);
+            case 160: return launch32<160>(a, general_mod, s);
+            case 192: return launch32<192>(a, general_mod, s);
+            case 224: return launch32<224>(a, general_mod, s);
+            case 256: return launch32<256>(a, general_mod, s);
             default: break;
         }
     }
@@ -2470,7 +2477,7 @@ hipError_t split_counter_slot(int slot, unsigned** ptr) {
 }
 
 bool flash_mfma_head_dim(int dtype, int D) {
-    if (dtype == DT_F32) return D == 32 || D == 64 || D == 96 || D == 128;
+    (void)dtype;  // every dtype: multiples of 32 up to 256
     return D % 32 == 0 && D >= 32 && D <= 256;
 }
 
@@ -2520,7 +2527,7 @@ const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile
 
 MfmaTiles flash_mfma_tiles(int dtype, int D, bool general_mod, bool tile_list, bool causal, int64_t bh,
                            int64_t query_tokens) {
-    if (dtype == DT_F32) return MfmaTiles{kBlockM32, kBlockNF32 * kTilesF32, kThreads32, false};
+    if (dtype == DT_F32) return MfmaTiles{kBlockM32, kBlockNF32 * (D > 128 ? 1 : kTilesF32), kThreads32, false};
     const bool paired = pairs_causal_tiles(causal, tile_list);
     const int bn = block_n16(D, general_mod, tile_list);
     const bool four =

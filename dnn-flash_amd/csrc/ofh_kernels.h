@@ -194,14 +194,13 @@ hipError_t launch_qk_score_mfma(const QkScoreArgs& a, int dtype, hipStream_t s);
 // builds its query tile's list in LDS (no tile_list launch, no workspace).
 size_t list_kernel_lds_bytes(int D, bool lds_list, int num_k_tiles);
 constexpr int kLdsListMaxTiles = 4096;  // key tiles of a list built in LDS
-// Head dims the MFMA kernels are built for: 32, 64, 96, 128 (fp32), every
-// multiple of 32 from 32 to 256 (bf16/fp16).
+// Head dims the MFMA kernels are built for: every multiple of 32 from 32 to
+// 256 (fp32 above 128 on one-block K/V tiles of 32 keys).
 bool flash_mfma_head_dim(int dtype, int D);
 // Head dim of the MFMA kernel that serves a call with head dims (D, Dv): the
 // larger rounded up to a multiple of 32 (the kernels zero-pad Q past D and
 // leave the output columns past Dv unwritten), or 0 when none does: bf16/fp16
-// need multiples of 8 up to 256, fp32 multiples of 4 up to 128 (16-byte row
-// chunks).
+// need multiples of 8, fp32 multiples of 4 (16-byte row chunks), up to 256.
 int flash_mfma_kernel_dim(int dtype, int D, int Dv);
 // threads: the workgroup size of the tiling the call runs (flash_mfma_tiles).
 const char* flash_mfma_kernel_name(int dtype, int D, bool general_mod, bool tile_list, int threads);

@@ -64,8 +64,8 @@ typedef enum ofh_bias_kind {
 } ofh_bias_kind;
 
 /* Which kernel family runs. AUTO picks the MFMA flash kernel when the shape
- * is supported (head_dim and value_dim multiples of 4 up to 128 for fp32, of
- * 8 up to 256 for bf16/fp16, D != Dv allowed: the kernel of max(D, Dv)
+ * is supported (head_dim and value_dim multiples of 4 for fp32 and of 8 for
+ * bf16/fp16, up to 256, D != Dv allowed: the kernel of max(D, Dv)
  * rounded up to 32 runs with the padding zeroed in place; 16-byte aligned
  * rows) and the rowwise kernel otherwise. ROWWISE is the exact two-pass
  * softmax of standard_attention, run on the GPU one query row per wavefront. */

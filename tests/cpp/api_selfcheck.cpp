@@ -307,9 +307,9 @@ int main() {
         of::standard_attention(q, k, v, shape, o);
     }, "bad BlockMask throws invalid_argument");
     expect_throw<std::runtime_error>([&] {
-        // fp32 MFMA kernels serve head dims up to 128
-        of::run_attention(of::AttentionBackendKind::FlashMfmaHip, sin_values(128 * 160, 0.f), sin_values(128 * 160, 1.f),
-                          sin_values(128 * 160, 2.f), of::AttentionShape{128, 128, 160, 160}, options);
+        // the MFMA kernels serve head dims up to 256
+        of::run_attention(of::AttentionBackendKind::FlashMfmaHip, sin_values(128 * 264, 0.f), sin_values(128 * 264, 1.f),
+                          sin_values(128 * 264, 2.f), of::AttentionShape{128, 128, 264, 264}, options);
     }, "unsupported MFMA shape throws runtime_error");
 
     std::printf("%s\n", failures == 0 ? "ALL OK" : "FAILURES");

@@ -151,7 +151,9 @@ def test_validation_messages(ofh):
                   F.OFH_ERROR_INVALID_ARGUMENT, "slopes")
     _expect_error(F, F.make_params(1, 1, 4, 4, 20, dtype=F.DTYPE_BF16, algorithm=F.ALGO_FLASH_MFMA),
                   F.OFH_ERROR_UNSUPPORTED, "flash MFMA kernel needs")
-    _expect_error(F, F.make_params(1, 1, 4, 4, 160, algorithm=F.ALGO_FLASH_MFMA),
+    _expect_error(F, F.make_params(1, 1, 4, 4, 264, algorithm=F.ALGO_FLASH_MFMA),
+                  F.OFH_ERROR_UNSUPPORTED, "flash MFMA kernel needs")
+    _expect_error(F, F.make_params(1, 1, 4, 4, 6, algorithm=F.ALGO_FLASH_MFMA),
                   F.OFH_ERROR_UNSUPPORTED, "flash MFMA kernel needs")
     _expect_error(F, F.make_params(1, 1, 4, 4, 64, max_key_splits=-1), F.OFH_ERROR_INVALID_ARGUMENT,
                   "max_key_splits")
@@ -221,7 +223,8 @@ def test_kernel_choice(ofh):
               mask_key_block_size=64, mask_query_blocks=5, mask_key_blocks=4),
          "flash_fwd_lockstep_kernel<f16,256,plain,list,4w>"),
         (dict(dtype=F.DTYPE_F32, head_dim=32), "flash_fwd_f32_rows16_kernel<32,plain>"),
-        (dict(dtype=F.DTYPE_F32, head_dim=256), "rowwise_fwd_kernel"),
+        (dict(dtype=F.DTYPE_F32, head_dim=256), "flash_fwd_mfma32_kernel<256,plain>"),
+        (dict(dtype=F.DTYPE_F32, head_dim=160, softcap=5.0), "flash_fwd_mfma32_kernel<160,general>"),
         (dict(dtype=F.DTYPE_F32, head_dim=96), "flash_fwd_f32_rows32_kernel<96,plain>"),
         (dict(dtype=F.DTYPE_F32, head_dim=96, shape=(8, 16, 1024, 300)), "flash_fwd_mfma32_kernel<96,plain>"),
         (dict(dtype=F.DTYPE_BF16, head_dim=96), "flash_fwd_lockstep_kernel<bf16,96,plain,8w,2x64keys>"),
@@ -262,7 +265,8 @@ def test_kernel_choice(ofh):
         (dict(dtype=F.DTYPE_BF16, head_dim=20), "rowwise_fwd_kernel"),
         (dict(dtype=F.DTYPE_F32, head_dim=6), "rowwise_fwd_kernel"),
         (dict(dtype=F.DTYPE_BF16, head_dim=264), "rowwise_fwd_kernel"),
-        (dict(dtype=F.DTYPE_F32, head_dim=64, value_dim=160), "rowwise_fwd_kernel"),
+        (dict(dtype=F.DTYPE_F32, head_dim=64, value_dim=160), "flash_fwd_mfma32_kernel<160,plain>"),
+        (dict(dtype=F.DTYPE_F32, head_dim=64, value_dim=264), "rowwise_fwd_kernel"),
         (dict(dtype=F.DTYPE_F32, head_dim=64, algorithm=F.ALGO_ROWWISE), "rowwise_fwd_kernel"),
     ]
     for kw, name in cases:

@@ -657,8 +657,6 @@ def test_rescale_with_live_accumulator(ofh, dt, D, sign, splits):
     negative scale (the min-based raw max of the unmasked tiles), each with
     one workgroup per query tile and with the key split (whose splits each
     rescale their own partial rows)."""
-    if dt == "f32" and D > 128:
-        pytest.skip("fp32 runs D > 128 on the rowwise kernel")
     N = 2048
     for causal, M in ((False, 300), (True, N)):
         dev, host, scale = rescale_inputs(dt, 1, 2, M, N, D, seed=D + int(sign > 0), sign=sign)
@@ -776,14 +774,13 @@ def test_eight_wavefronts_wide_head_dims(ofh, dt, D):
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
 @pytest.mark.parametrize("D", [32, 96, 160, 192, 224, 256])
 def test_head_dims_beyond_64_and_128(ofh, dt, D):
-    """The MFMA kernels at D = 32 and 96 (bf16/fp16/fp32) and 160 ... 256
-    (bf16/fp16; unswizzled rows when D is not a power of two): ALiBi +
+    """The MFMA kernels at D = 32 and 96 and 160 ... 256 (bf16/fp16:
+    unswizzled rows when D is not a power of two; fp32 above 128: one-block
+    K/V tiles of 32 keys, one wavefront per SIMD): ALiBi +
     soft-cap, a dense bias, a block mask (the list kernel), and the lazy
     rescale with a live accumulator and a negative scale, each with one
     workgroup per query tile and with the key split."""
     F = ofh
-    if dt == "f32" and D > 128:
-        pytest.skip("fp32 runs D > 128 on the rowwise kernel")
     B, H, M, N = 1, 2, 300, 700
     code = {"f32": F.DTYPE_F32, "bf16": F.DTYPE_BF16, "f16": F.DTYPE_F16}[dt]
     assert F.launch_info(F.make_params(B, H, M, N, D, dtype=code)).algorithm == F.ALGO_FLASH_MFMA
@@ -825,8 +822,6 @@ PADDED_DIMS = [(16, 16), (48, 48), (80, 80), (112, 112), (144, 144), (64, 48), (
 def test_mfma_padded_head_dims(ofh, dt, dims):
     D, Dv = dims
     F = ofh
-    if dt == "f32" and max(D, Dv) > 128:
-        pytest.skip("fp32 MFMA kernels serve head dims up to 128")
     B, H, M, N = 1, 2, 300, 700
     code = {"f32": F.DTYPE_F32, "bf16": F.DTYPE_BF16, "f16": F.DTYPE_F16}[dt]
     info = F.launch_info(F.make_params(B, H, M, N, D, Dv, dtype=code))
